@@ -1,0 +1,683 @@
+// Row quantization kernels for gfx950: per-token asymmetric activation codes
+// and per-channel symmetric weight codes, optionally preceded by the online
+// block-Hadamard rotation, with int4 nibble packing.
+//
+// Rules restated (reference paths):
+//   activations  core/quantization.py:13-21, kernel/w4a4.cu:20-54
+//   weights      core/quantization.py:7-11, pack_int4 :31-40
+//   rotation     the fold rule of core/linear.py:34-37 with R = H_128/sqrt(128)
+//                split as (W H/128)(H x): activations get the unnormalised
+//                Sylvester transform, weights the exact 1/128 scale.
+//
+// Work layout.  A row of K elements is cut into 128-element blocks.  Four
+// lanes (a "quad") own a block: lane r of the quad holds four 8-element
+// chunks j = 0..3 at block offsets j*32 + r*8, each chunk fetched with one
+// 16-byte load (fp16).  Block index bits 0-2 are therefore in-chunk, bits 3-4
+// are the lane within the quad and bits 5-6 are the chunk: the transform's
+// seven butterfly stages run as 3 in-register + 2 DPP quad_perm + 2
+// in-register stages, and a load instruction of the wave reads 16 quads x 64
+// contiguous bytes.  A row is spread over WPR waves (16*WPR quads), each quad
+// taking blocks quad, quad + 16*WPR, ... up to ITERS of them; the whole row
+// stays in VGPRs, so x is read from HBM exactly once.  Rows longer than the
+// register capacity use the two-pass streaming kernel at the end.
+//
+// Exact division at bandwidth.  The reference computes
+// code = clamp(round_half_even(fl(fl(x / s) + z))).  Per element we use
+// t = fma(x, y, z) with y = fl(1 / s) computed once per row.  Writing
+// Q = x / s, |x*y - Q| <= 2^-24 |Q| and |fl(Q) - Q| <= 2^-24 |Q|, and both
+// sums are rounded once more, so |t - fl(fl(Q) + z)| <= 2^-23 |Q| + ulp(T)
+// with T = |Q| + qmax.  If t lies further than delta = (|Q|max + 16) * 2^-21
+// (a 2x margin over that bound) from every half-integer, t and the exact
+// value round to the same integer; a lane that sees any element closer than
+// that recomputes all its elements with IEEE division (rare: ~1e-4 of lanes).
+// Clamping commutes with rounding because the bounds are integers.
+
+#include "../../include/dscq.h"
+#include "common.h"
+
+namespace dscq {
+namespace {
+
+constexpr int kThreads = 256;
+
+enum Mode { kAct = 0, kWgt = 1 };
+
+struct RowArgs {
+  const void* x;       // [M, K] T
+  int64_t M, K, KP, MP;
+  int nblk;            // ceil(KP / 128)
+  float clip;
+  float qmax;          // act: 2^bits - 1;  weight: 2^(bits-1) - 1
+  uint8_t* packed;     // [MP, KP/2] or null
+  uint8_t* codes;      // [MP, KP] or null (u8 act codes / int8 weight codes)
+  float* scales;       // [MP]
+  int32_t* zeros;      // [MP] act zero-points or null
+  int32_t* sums;       // [MP] weight code sums or null
+  int vec;             // rows 16-byte aligned and K % 8 == 0
+};
+
+// ------------------------------------------------------------------ loading
+
+__device__ __forceinline__ void cvt8(const uint4 r, float v[8]) {
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __half2float(__ushort_as_half((unsigned short)(w[i] & 0xFFFFu)));
+    v[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(w[i] >> 16)));
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void load_chunk(const T* row, int64_t e0, int64_t K,
+                                           bool vec, float v[8]);
+
+template <>
+__device__ __forceinline__ void load_chunk<__half>(const __half* row, int64_t e0,
+                                                   int64_t K, bool vec,
+                                                   float v[8]) {
+  if (vec) {
+    if (e0 < K) {
+      cvt8(*reinterpret_cast<const uint4*>(row + e0), v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (e0 + i < K) ? __half2float(row[e0 + i]) : 0.0f;
+  }
+}
+
+template <>
+__device__ __forceinline__ void load_chunk<float>(const float* row, int64_t e0,
+                                                  int64_t K, bool vec, float v[8]) {
+  if (vec) {
+    if (e0 < K) {
+      const float4 a = *reinterpret_cast<const float4*>(row + e0);
+      const float4 b = *reinterpret_cast<const float4*>(row + e0 + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (e0 + i < K) ? row[e0 + i] : 0.0f;
+  }
+}
+
+// -------------------------------------------------------- block transform
+
+// Butterfly (u, w) -> (u + w, u - w) on index bit `h` within one chunk.
+__device__ __forceinline__ void fwht_chunk(float v[8]) {
+#pragma unroll
+  for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (!(i & h)) {
+        const float u = v[i], w = v[i + h];
+        v[i] = u + w;
+        v[i + h] = u - w;
+      }
+}
+
+// Stages for index bits 3..6 of one block held as c[4][8] by a quad lane.
+// Bits 3-4 pair lanes r^1 and r^2: the lane with the bit clear keeps
+// own + partner, the other partner - own, i.e. fma(+-1, own, partner), which
+// rounds exactly like the plain add / subtract.
+__device__ __forceinline__ void fwht_block_tail(float c[4][8], int r) {
+  const float s1 = (r & 1) ? -1.0f : 1.0f;
+  const float s2 = (r & 2) ? -1.0f : 1.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[j][i] = __builtin_fmaf(s1, c[j][i], dpp_f32<kDppQuadXor1>(c[j][i]));
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[j][i] = __builtin_fmaf(s2, c[j][i], dpp_f32<kDppQuadXor2>(c[j][i]));
+#pragma unroll
+  for (int h = 1; h < 4; h <<= 1)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (!(j & h)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float u = c[j][i], w = c[j + h][i];
+          c[j][i] = u + w;
+          c[j + h][i] = u - w;
+        }
+      }
+}
+
+// ------------------------------------------------------------ quantization
+
+struct RowScale {
+  float scale, y, zf, qmax, thr;
+};
+
+// Activation chunk -> bytes u = q (evens: elements 0,2,4,6; odds: 1,3,5,7).
+// Fast path; returns in *dmax the largest |t - round(t)| seen.
+__device__ __forceinline__ void act_chunk_fast(const float v[8], const RowScale& rs,
+                                               uint32_t& ev, uint32_t& od,
+                                               float& dmax) {
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float t = __builtin_amdgcn_fmed3f(__builtin_fmaf(v[i], rs.y, rs.zf), 0.0f, rs.qmax);
+    q[i] = __builtin_rintf(t);
+    dmax = fmaxf(dmax, fabsf(t - q[i]));
+  }
+  ev = put_u8<0>(q[0], 0u); ev = put_u8<1>(q[2], ev); ev = put_u8<2>(q[4], ev); ev = put_u8<3>(q[6], ev);
+  od = put_u8<0>(q[1], 0u); od = put_u8<1>(q[3], od); od = put_u8<2>(q[5], od); od = put_u8<3>(q[7], od);
+}
+
+// Activation chunk with correctly rounded division (the reference's exact rule).
+__device__ __forceinline__ void act_chunk_exact(const float v[8], const RowScale& rs,
+                                                uint32_t& ev, uint32_t& od) {
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    q[i] = __builtin_amdgcn_fmed3f(__builtin_rintf(v[i] / rs.scale + rs.zf), 0.0f, rs.qmax);
+  ev = put_u8<0>(q[0], 0u); ev = put_u8<1>(q[2], ev); ev = put_u8<2>(q[4], ev); ev = put_u8<3>(q[6], ev);
+  od = put_u8<0>(q[1], 0u); od = put_u8<1>(q[3], od); od = put_u8<2>(q[5], od); od = put_u8<3>(q[7], od);
+}
+
+// Weight chunk -> bytes u = c + qmax + 1 (so u ^ 8 is the int4 nibble when
+// qmax = 7) and the chunk's code sum.
+__device__ __forceinline__ void wgt_chunk(const float v[8], const RowScale& rs,
+                                          uint32_t& ev, uint32_t& od, int& sum) {
+  float c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    c[i] = __builtin_amdgcn_fmed3f(__builtin_rintf(v[i] / rs.scale), -rs.qmax, rs.qmax);
+    sum += (int)c[i];
+  }
+  const float off = rs.qmax + 1.0f;
+  ev = put_u8<0>(c[0] + off, 0u); ev = put_u8<1>(c[2] + off, ev);
+  ev = put_u8<2>(c[4] + off, ev); ev = put_u8<3>(c[6] + off, ev);
+  od = put_u8<0>(c[1] + off, 0u); od = put_u8<1>(c[3] + off, od);
+  od = put_u8<2>(c[5] + off, od); od = put_u8<3>(c[7] + off, od);
+}
+
+template <int MODE>
+__device__ __forceinline__ RowScale row_scale(float mn, float mx, float clip,
+                                              float qmax) {
+  RowScale rs;
+  rs.qmax = qmax;
+  if (MODE == kAct) {
+    // core/quantization.py:15-19; kernel/w4a4.cu:42-44.
+    const float lo = mn * clip, hi = mx * clip;
+    rs.scale = fmaxf((hi - lo) / qmax, 1e-8f);
+    rs.zf = __builtin_amdgcn_fmed3f(__builtin_rintf(-lo / rs.scale), 0.0f, qmax);
+    rs.y = 1.0f / rs.scale;
+    const float qbound = fmaxf(mx, -mn) / rs.scale;
+    rs.thr = 0.5f - (qbound + 16.0f) * 0x1p-21f;
+  } else {
+    // core/quantization.py:9 (amax * clip / bound, then the 1e-8 floor).
+    rs.scale = fmaxf(mx * clip / qmax, 1e-8f);
+    rs.zf = 0.0f;
+    rs.y = 0.0f;
+    rs.thr = 1.0f;
+  }
+  return rs;
+}
+
+// Outputs of one chunk: packed nibbles and / or codes.  Byte i of ev / od is
+// u = q (activations) or u = c + qmax + 1 (weights) for element 2i / 2i + 1.
+template <int MODE>
+__device__ __forceinline__ void store_chunk(const RowArgs& a, int64_t row,
+                                            int64_t e0, uint32_t ev, uint32_t od) {
+  if (e0 >= a.KP) return;
+  if (a.packed) {
+    // act: (q - 8) & 15 == q ^ 8;  weight: c & 15 == (c + 8) ^ 8.
+    const uint32_t p = (ev | (od << 4)) ^ 0x88888888u;
+    *reinterpret_cast<uint32_t*>(a.packed + row * (a.KP / 2) + e0 / 2) = p;
+  }
+  if (a.codes) {
+    uint32_t lo = __builtin_amdgcn_perm(od, ev, 0x05010400u);
+    uint32_t hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);
+    if (MODE == kWgt) {
+      // Per byte (no borrow between bytes): int8 code = u - (qmax + 1).
+      const uint32_t off = (uint32_t)(a.qmax + 1.0f);
+      uint32_t l2 = 0, h2 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        l2 |= ((((lo >> (8 * i)) & 0xFFu) - off) & 0xFFu) << (8 * i);
+        h2 |= ((((hi >> (8 * i)) & 0xFFu) - off) & 0xFFu) << (8 * i);
+      }
+      lo = l2;
+      hi = h2;
+    }
+    uint2 w;
+    w.x = lo;
+    w.y = hi;
+    *reinterpret_cast<uint2*>(a.codes + row * a.KP + e0) = w;
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ void write_row_meta(const RowArgs& a, int64_t row, bool real,
+                                               const RowScale& rs, int sum) {
+  if (MODE == kAct) {
+    a.scales[row] = rs.scale;
+    if (a.zeros) a.zeros[row] = (int32_t)rs.zf;
+  } else {
+    // Padded weight rows carry scale 0 and sum 0.
+    a.scales[row] = real ? rs.scale : 0.0f;
+    if (a.sums) a.sums[row] = real ? sum : 0;
+  }
+}
+
+// --------------------------------------------------------- register kernel
+
+template <typename T, bool ROT, int MODE, int WPR, int ITERS>
+__global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
+  constexpr int ROWS = (kThreads / 64) / WPR;
+  constexpr int NQ = 16 * WPR;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row_in_wg = wave / WPR;
+  const int wave_in_row = wave % WPR;
+  const int64_t row = (int64_t)blockIdx.x * ROWS + row_in_wg;
+  const bool live = row < a.MP;
+  const bool real = row < a.M;
+  const int quad = wave_in_row * 16 + (lane >> 2);
+  const int r = lane & 3;
+  const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.K;
+  const bool vec = a.vec != 0;
+
+  float v[ITERS][4][8];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int b = quad + it * NQ;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
+      if (real && b < a.nblk) {
+        load_chunk<T>(xrow, e0, a.K, vec, v[it][j]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[it][j][i] = 0.0f;
+      }
+    }
+  }
+
+  if (ROT) {
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fwht_chunk(v[it][j]);
+      fwht_block_tail(v[it], r);
+      if (MODE == kWgt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[it][j][i] *= 0.0078125f;  // 1/128, exact
+      }
+    }
+  }
+
+  float mn = 0.0f, mx = 0.0f;
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (MODE == kAct) {
+          mn = fminf(mn, v[it][j][i]);
+          mx = fmaxf(mx, v[it][j][i]);
+        } else {
+          mx = fmaxf(mx, fabsf(v[it][j][i]));
+        }
+      }
+  if (MODE == kAct) mn = wave_min(mn);
+  mx = wave_max(mx);
+  if (WPR > 1) {
+    __shared__ float red[2][kThreads / 64];
+    if (lane == 0) {
+      red[0][wave] = mn;
+      red[1][wave] = mx;
+    }
+    __syncthreads();
+    mn = red[0][row_in_wg * WPR];
+    mx = red[1][row_in_wg * WPR];
+#pragma unroll
+    for (int w = 1; w < WPR; ++w) {
+      mn = fminf(mn, red[0][row_in_wg * WPR + w]);
+      mx = fmaxf(mx, red[1][row_in_wg * WPR + w]);
+    }
+  }
+  const RowScale rs = row_scale<MODE>(mn, mx, a.clip, a.qmax);
+
+  uint32_t ev[ITERS][4], od[ITERS][4];
+  int sum = 0;
+  if (MODE == kAct) {
+    float dmax = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) act_chunk_fast(v[it][j], rs, ev[it][j], od[it][j], dmax);
+    if (dmax > rs.thr) {
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) act_chunk_exact(v[it][j], rs, ev[it][j], od[it][j]);
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wgt_chunk(v[it][j], rs, ev[it][j], od[it][j], sum);
+    if (a.sums) {
+      sum = wave_sum_i32(sum);
+      if (WPR > 1) {
+        // Reached by every wave of the workgroup (no early exits above).
+        __shared__ int sred[kThreads / 64];
+        if (lane == 0) sred[wave] = sum;
+        __syncthreads();
+        sum = 0;
+#pragma unroll
+        for (int w = 0; w < WPR; ++w) sum += sred[row_in_wg * WPR + w];
+      }
+    }
+  }
+  if (!live) return;
+
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int b = quad + it * NQ;
+    if (b < a.nblk) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        store_chunk<MODE>(a, row, (int64_t)b * 128 + j * 32 + r * 8, ev[it][j], od[it][j]);
+    }
+  }
+  if (wave_in_row == 0 && lane == 0) write_row_meta<MODE>(a, row, real, rs, sum);
+}
+
+// ------------------------------------------------------ streaming kernel
+// For rows longer than the register kernel holds (K > 32768): one row per
+// workgroup, 64 quads walk the row's blocks twice -- once for min / max, once
+// to quantize -- re-reading x (the second pass mostly hits L2).
+
+template <typename T, bool ROT, int MODE>
+__device__ __forceinline__ void load_block(const RowArgs& a, const T* xrow, bool real,
+                                           int b, int r, float c[4][8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
+    if (real && b < a.nblk) {
+      load_chunk<T>(xrow, e0, a.K, a.vec != 0, c[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[j][i] = 0.0f;
+    }
+  }
+  if (ROT) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fwht_chunk(c[j]);
+    fwht_block_tail(c, r);
+    if (MODE == kWgt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[j][i] *= 0.0078125f;
+    }
+  }
+}
+
+template <typename T, bool ROT, int MODE>
+__global__ __launch_bounds__(kThreads) void row_quant_stream_kernel(RowArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  const bool real = row < a.M;
+  const int quad = wave * 16 + (lane >> 2);
+  const int r = lane & 3;
+  const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.K;
+  constexpr int NQ = 64;
+  // The loop bound is uniform across the workgroup, so every lane runs the
+  // same number of iterations and the DPP partners are always live.
+  const int rounds = (a.nblk + NQ - 1) / NQ;
+
+  float mn = 0.0f, mx = 0.0f;
+  for (int it = 0; it < rounds; ++it) {
+    float c[4][8];
+    load_block<T, ROT, MODE>(a, xrow, real, quad + it * NQ, r, c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (MODE == kAct) {
+          mn = fminf(mn, c[j][i]);
+          mx = fmaxf(mx, c[j][i]);
+        } else {
+          mx = fmaxf(mx, fabsf(c[j][i]));
+        }
+      }
+  }
+  if (MODE == kAct) mn = wave_min(mn);
+  mx = wave_max(mx);
+  __shared__ float red[2][kThreads / 64];
+  if (lane == 0) {
+    red[0][wave] = mn;
+    red[1][wave] = mx;
+  }
+  __syncthreads();
+  mn = fminf(fminf(red[0][0], red[0][1]), fminf(red[0][2], red[0][3]));
+  mx = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+  const RowScale rs = row_scale<MODE>(mn, mx, a.clip, a.qmax);
+
+  int sum = 0;
+  for (int it = 0; it < rounds; ++it) {
+    const int b = quad + it * NQ;
+    float c[4][8];
+    load_block<T, ROT, MODE>(a, xrow, real, b, r, c);
+    uint32_t ev[4], od[4];
+    if (MODE == kAct) {
+      float dmax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) act_chunk_fast(c[j], rs, ev[j], od[j], dmax);
+      if (dmax > rs.thr) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) act_chunk_exact(c[j], rs, ev[j], od[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wgt_chunk(c[j], rs, ev[j], od[j], sum);
+    }
+    if (b < a.nblk) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        store_chunk<MODE>(a, row, (int64_t)b * 128 + j * 32 + r * 8, ev[j], od[j]);
+    }
+  }
+  if (MODE == kWgt && a.sums) {
+    sum = wave_sum_i32(sum);
+    __shared__ int sred[kThreads / 64];
+    if (lane == 0) sred[wave] = sum;
+    __syncthreads();
+    sum = sred[0] + sred[1] + sred[2] + sred[3];
+  }
+  if (wave == 0 && lane == 0) write_row_meta<MODE>(a, row, real, rs, sum);
+}
+
+// ------------------------------------------------------- small kernels
+
+// codes u8 [MP, KP] (0..15) -> packed [MP, KP/2]; kernel/w4a4.cu:65-68.
+// Each thread packs 16 codes (one 16-byte load) into 8 bytes.
+__global__ __launch_bounds__(kThreads) void pack_codes_kernel(const uint8_t* codes,
+                                                              uint8_t* packed,
+                                                              int64_t n16) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n16) return;
+  const uint4 c = reinterpret_cast<const uint4*>(codes)[i];
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+  uint32_t outw[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // bytes [q0 q1 q2 q3] [q4 q5 q6 q7] -> evens / odds, then nibbles.
+    const uint32_t ev = __builtin_amdgcn_perm(w[2 * h + 1], w[2 * h], 0x06040200u);
+    const uint32_t od = __builtin_amdgcn_perm(w[2 * h + 1], w[2 * h], 0x07050301u);
+    outw[h] = ((ev & 0x0F0F0F0Fu) | ((od & 0x0F0F0F0Fu) << 4)) ^ 0x88888888u;
+  }
+  uint2 o;
+  o.x = outw[0];
+  o.y = outw[1];
+  reinterpret_cast<uint2*>(packed)[i] = o;
+}
+
+// pack_int4, core/quantization.py:31-40: int8 [R, C] -> u8 [R, ceil(C/2)].
+__global__ __launch_bounds__(kThreads) void pack_int4_kernel(const int8_t* codes,
+                                                             int64_t R, int64_t C,
+                                                             uint8_t* packed) {
+  const int64_t CB = (C + 1) / 2;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= R * CB) return;
+  const int64_t r = i / CB, j = i % CB;
+  const int lo = codes[r * C + 2 * j] & 15;
+  const int hi = (2 * j + 1 < C) ? (codes[r * C + 2 * j + 1] & 15) : 0;
+  packed[i] = (uint8_t)(lo | (hi << 4));
+}
+
+// unpack_int4, core/quantization.py:42-45: u8 [R, CB] -> int8 [R, width].
+__global__ __launch_bounds__(kThreads) void unpack_int4_kernel(const uint8_t* packed,
+                                                               int64_t R, int64_t CB,
+                                                               int64_t width,
+                                                               int8_t* codes) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= R * width) return;
+  const int64_t r = i / width, c = i % width;
+  const int nib = (packed[r * CB + c / 2] >> ((c & 1) * 4)) & 15;
+  codes[i] = (int8_t)(nib >= 8 ? nib - 16 : nib);
+}
+
+}  // namespace
+}  // namespace dscq
+
+// ================================================================ host side
+
+namespace dscq {
+namespace {
+
+template <typename T, bool ROT, int MODE>
+int launch_rows_typed(const RowArgs& a, int wpr, int iters, hipStream_t stream) {
+  if (wpr == 0) {
+    hipLaunchKernelGGL((row_quant_stream_kernel<T, ROT, MODE>), dim3((unsigned)a.MP),
+                       dim3(kThreads), 0, stream, a);
+    return launch_status("row_quant_stream_kernel");
+  }
+  const int rows_per_wg = (kThreads / 64) / wpr;
+  const dim3 grid((unsigned)((a.MP + rows_per_wg - 1) / rows_per_wg));
+#define DSCQ_ROWS(W, I)                                                                \
+  if (wpr == W && iters == I) {                                                        \
+    hipLaunchKernelGGL((row_quant_kernel<T, ROT, MODE, W, I>), grid, dim3(kThreads), 0, \
+                       stream, a);                                                     \
+    return launch_status("row_quant_kernel");                                         \
+  }
+  DSCQ_ROWS(1, 1) DSCQ_ROWS(1, 2) DSCQ_ROWS(1, 4)
+  DSCQ_ROWS(2, 1) DSCQ_ROWS(2, 2) DSCQ_ROWS(2, 4)
+  DSCQ_ROWS(4, 1) DSCQ_ROWS(4, 2) DSCQ_ROWS(4, 4)
+#undef DSCQ_ROWS
+  return fail("internal: no row kernel for wpr=%d iters=%d", wpr, iters);
+}
+
+// Register-kernel shape for a row of nblk 128-blocks: waves per row and
+// blocks per quad.  Many rows: one wave per row (no barriers); few rows:
+// spread each row over more waves.  wpr = 0 selects the streaming kernel.
+void pick_shape(int64_t MP, int nblk, int* wpr, int* iters) {
+  static const int kCand[9][2] = {{1, 1}, {1, 2}, {2, 1}, {1, 4}, {2, 2},
+                                  {4, 1}, {2, 4}, {4, 2}, {4, 4}};
+  const bool many_rows = MP >= 1024;
+  int best = -1;
+  for (int c = 0; c < 9; ++c) {
+    if (16 * kCand[c][0] * kCand[c][1] < nblk) continue;
+    if (best < 0) {
+      best = c;
+      continue;
+    }
+    const int w = kCand[c][0], i = kCand[c][1];
+    const int bw = kCand[best][0], bi = kCand[best][1];
+    const bool better = many_rows ? (w < bw || (w == bw && i < bi))
+                                  : (i < bi || (i == bi && w < bw));
+    if (better) best = c;
+  }
+  if (best < 0) {
+    *wpr = 0;
+    *iters = 0;
+  } else {
+    *wpr = kCand[best][0];
+    *iters = kCand[best][1];
+  }
+}
+
+}  // namespace
+
+// Launches one row-quantization pass.  mode 0: activations (qmax = 2^bits-1),
+// 1: weights (qmax = 2^(bits-1)-1).  Rows M..MP-1 are written as padding.
+int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float clip,
+              int mode, float qmax, int rotate_block, uint8_t* packed, uint8_t* codes,
+              float* scales, int32_t* zeros, int32_t* sums, hipStream_t stream) {
+  RowArgs a;
+  a.x = x;
+  a.M = M;
+  a.K = K;
+  a.KP = ceil_to(K, 64);
+  a.MP = MP;
+  a.nblk = (int)((a.KP + 127) / 128);
+  a.clip = clip;
+  a.qmax = qmax;
+  a.packed = packed;
+  a.codes = codes;
+  a.scales = scales;
+  a.zeros = zeros;
+  a.sums = sums;
+  const int esize = dtype == DSCQ_F16 ? 2 : 4;
+  a.vec = (K % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
+          ((K * esize) % 16 == 0);
+  int wpr, iters;
+  pick_shape(MP, a.nblk, &wpr, &iters);
+  const bool rot = rotate_block != 0;
+#define DSCQ_T(T)                                                                    \
+  if (rot)                                                                           \
+    return mode == kAct ? launch_rows_typed<T, true, kAct>(a, wpr, iters, stream)    \
+                        : launch_rows_typed<T, true, kWgt>(a, wpr, iters, stream);   \
+  return mode == kAct ? launch_rows_typed<T, false, kAct>(a, wpr, iters, stream)     \
+                      : launch_rows_typed<T, false, kWgt>(a, wpr, iters, stream);
+  if (dtype == DSCQ_F16) {
+    DSCQ_T(__half)
+  }
+  DSCQ_T(float)
+#undef DSCQ_T
+}
+
+int pack_codes(const uint8_t* codes, uint8_t* packed, int64_t MP, int64_t KP,
+               hipStream_t stream) {
+  const int64_t n16 = MP * KP / 16;
+  hipLaunchKernelGGL(pack_codes_kernel, dim3((unsigned)((n16 + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, codes, packed, n16);
+  return launch_status("pack_codes_kernel");
+}
+
+int pack_int4(const int8_t* codes, int64_t R, int64_t C, uint8_t* packed,
+              hipStream_t stream) {
+  const int64_t n = R * ((C + 1) / 2);
+  if (n == 0) return DSCQ_OK;
+  hipLaunchKernelGGL(pack_int4_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, codes, R, C, packed);
+  return launch_status("pack_int4_kernel");
+}
+
+int unpack_int4(const uint8_t* packed, int64_t R, int64_t CB, int64_t width,
+                int8_t* codes, hipStream_t stream) {
+  const int64_t n = R * width;
+  if (n == 0) return DSCQ_OK;
+  hipLaunchKernelGGL(unpack_int4_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, packed, R, CB, width, codes);
+  return launch_status("unpack_int4_kernel");
+}
+
+}  // namespace dscq

@@ -1,0 +1,159 @@
+/*
+ * dscq.h — C ABI of the MI355X (gfx950) W4A4 linear-layer library
+ * (libdscq.so, built from dscquant_amd/csrc/).
+ *
+ * Plain pointers and sizes only.  Every device pointer is HIP device memory
+ * on the current device; `stream` is a hipStream_t (NULL = the default
+ * stream).  Calls are asynchronous on `stream` and never synchronize.
+ *
+ * Return value: DSCQ_OK (0) on success; DSCQ_EINVAL (-1) when an argument
+ * check fails (nothing was launched; the message is in dscq_last_error());
+ * otherwise the positive hipError_t returned by the launch.
+ *
+ * Padded layout (the reference extension's, kernel/w4a4.cu:170,196):
+ *   MP = ceil(M / 8) * 8,  NP = ceil(N / 8) * 8,  KP = ceil(K / 64) * 64.
+ * Packed int4 matrices are row-major u8 [rows, KP/2]; byte j of a row holds
+ * element 2j in its low nibble and 2j+1 in its high nibble.
+ */
+#ifndef DSCQ_H
+#define DSCQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSCQ_OK 0
+#define DSCQ_EINVAL (-1)
+
+/* Element types of floating-point tensors. */
+#define DSCQ_F16 0
+#define DSCQ_F32 1
+
+/*
+ * Per-token activation quantization + int4 packing, optionally preceded by
+ * an online block rotation.
+ * Replaces the reference extension's `quantize(x, clip, fused)`
+ * (kernel/w4a4.cu:164-187, kernels :20-68) and follows the rule of
+ * activation_codes (core/quantization.py:13-21).
+ *
+ *   x        [M, K] fp16 or fp32 (x_dtype), row-major, contiguous.
+ *   clip     activation clip ratio, 0.5 <= clip <= 1 (w4a4.cu:168).
+ *   fused    1: one kernel writes `packed` directly (w4a4.cu:177);
+ *            0: a codes kernel writes `codes` [MP, KP] u8 (values 0..15),
+ *               then a pack kernel writes `packed` (w4a4.cu:178-185).
+ *   rotate_block  0 = no rotation; 128 = unnormalised Sylvester Hadamard
+ *            H_128 applied to every 128-wide block of each row before
+ *            quantization (K must be a multiple of 128).  Pair it with
+ *            weights packed by dscq_pack_weight(..., rotate_block = 128).
+ *   packed   out u8 [MP, KP/2]; nibble = (q - 8) & 15.
+ *   scales   out f32 [MP]; zeros out i32 [MP] (padded rows: 1e-8, 0).
+ *   codes    scratch/out u8 [MP, KP] when fused == 0, else ignored (may be NULL).
+ * Limits (w4a4.cu:166): 1 <= M <= 65535, 1 <= K <= 1048576.
+ */
+int dscq_quantize(const void* x, int x_dtype, int64_t M, int64_t K, float clip,
+                  int fused, int rotate_block, uint8_t* packed, float* scales,
+                  int32_t* zeros, uint8_t* codes, void* stream);
+
+/*
+ * Activation codes with any bit width 2..8 (no packing), the GPU form of
+ * activation_codes (core/quantization.py:13-21) on the padded layout.
+ *   codes  out u8 [MP, KP] in [0, 2^bits - 1] (padded k / rows: the row's zero)
+ *   scales out f32 [MP], zeros out i32 [MP].
+ * clip may be any value in (0, 1].  rotate_block as in dscq_quantize.
+ */
+int dscq_activation_codes(const void* x, int x_dtype, int64_t M, int64_t K,
+                          float clip, int bits, int rotate_block,
+                          uint8_t* codes, float* scales, int32_t* zeros,
+                          void* stream);
+
+/*
+ * Weight-side glue of the W4A4 GEMM: per-output-channel symmetric int4 codes
+ * (weight_codes, core/quantization.py:7-11, bits = 4), packed as pack_int4
+ * (core/quantization.py:31-40) into the padded operand `b` of dscq_matmul,
+ * plus the per-channel scale `sw` and code sums `sums` the epilogue needs
+ * (kernel/w4a4.cu:74-75, shape contract :195-200).  The reference leaves
+ * this glue unwritten; its layout is pinned by matmul's checks.
+ *   w       [N, K] fp16 or fp32 (w_dtype), row-major.
+ *   clip    weight clip ratio in (0, 1].
+ *   rotate_block 0, or 128: quantize W' = W H_128 / 128 (blockwise, exact
+ *           power-of-two scale), the fold that pairs with the rotated
+ *           activations of dscq_quantize (rule of core/linear.py:34-37).
+ *   packed  out u8 [NP, KP/2] (padding: code 0); sw out f32 [NP];
+ *   sums    out i32 [NP] (padded rows: sw 0, sums 0).
+ *   codes   optional out int8 [NP, KP] (the signed codes), may be NULL.
+ * Limits: 1 <= N <= 1048576, 1 <= K <= 1048576.
+ */
+int dscq_pack_weight(const void* w, int w_dtype, int64_t N, int64_t K,
+                     float clip, int rotate_block, uint8_t* packed, float* sw,
+                     int32_t* sums, int8_t* codes, void* stream);
+
+/*
+ * Weight codes with any bit width 2..8 (no packing): codes int8 [NP, KP] in
+ * [-(2^(bits-1)-1), 2^(bits-1)-1], scales f32 [NP].  The GPU form of
+ * weight_codes (core/quantization.py:7-11).  rotate_block as in
+ * dscq_pack_weight.
+ */
+int dscq_weight_codes(const void* w, int w_dtype, int64_t N, int64_t K,
+                      float clip, int bits, int rotate_block, int8_t* codes,
+                      float* scales, void* stream);
+
+/*
+ * Packed-int4 x packed-int4 GEMM with int32 accumulation and the fused
+ * zero-point / scale / bias epilogue.  Replaces the reference extension's
+ * `matmul(a, b, sx, zx, sw, sums, bias, M, N, fused, force_decode, fp32)`
+ * (kernel/w4a4.cu:189-225, kernels :70-161):
+ *   raw[m, n] = sum_{k < KP} (a nibble - 16*(a nibble >= 8)) * (b nibble ...)
+ *   out[m, n] = (float)(raw + (8 - zx[m]) * sums[n]) * sx[m] * sw[n] (+ bias[n])
+ *   a     u8 [>= MP, KP/2] activations (dscq_quantize's `packed`).
+ *   b     u8 [>= NP, KP/2] weights (dscq_pack_weight's `packed`).
+ *   sx    f32 [>= MP], zx i32 [>= MP], sw f32 [>= NP], sums i32 [>= NP].
+ *   bias  NULL or [N] of the output type.
+ *   KP    packed width * 2; a multiple of 64, 64 <= KP <= 1048576.
+ *   fused 1: out only (raw may be NULL); 0: out and raw [M, N] int32
+ *         (the reference's raw-accumulator mode).
+ *   force_decode  selects the skinny-M kernel (the reference's decode_gemm)
+ *         regardless of M; it is also chosen for M < 8.  Results are
+ *         identical either way.
+ *   out_fp32  0: out is fp16 [M, N]; 1: fp32.
+ * Limits (w4a4.cu:197): 1 <= M <= 65535, N >= 1.
+ */
+int dscq_matmul(const uint8_t* a, const uint8_t* b, const float* sx,
+                const int32_t* zx, const float* sw, const int32_t* sums,
+                const void* bias, int64_t M, int64_t N, int64_t KP, int fused,
+                int force_decode, int out_fp32, void* out, int32_t* raw,
+                void* stream);
+
+/*
+ * Standalone int4 packer for signed codes already in [-8, 7]: the GPU form
+ * of pack_int4 (core/quantization.py:31-40; range checking is the caller's,
+ * see dscquant_amd.core.quantization.pack_int4).
+ *   codes int8 [R, C] -> packed u8 [R, ceil(C/2)] (odd width padded with 0).
+ */
+int dscq_pack_int4(const int8_t* codes, int64_t R, int64_t C, uint8_t* packed,
+                   void* stream);
+
+/* The GPU form of unpack_int4 (core/quantization.py:42-45):
+ * packed u8 [R, CB] -> codes int8 [R, width], width <= 2*CB. */
+int dscq_unpack_int4(const uint8_t* packed, int64_t R, int64_t CB,
+                     int64_t width, int8_t* codes, void* stream);
+
+/*
+ * 1 if the current HIP device is a gfx950 (MI355X-class) GPU the kernels
+ * were built for, 0 if not, negative hipError_t if no device is usable.
+ * Replaces the SM75-89 capability check of kernel/w4a4.cu:204-206.
+ */
+int dscq_device_supported(void);
+
+/* Message of the last DSCQ_EINVAL / launch failure on this thread. */
+const char* dscq_last_error(void);
+
+/* Library version string. */
+const char* dscq_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSCQ_H */

@@ -1,0 +1,52 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+@pytest.fixture(scope="session", autouse=True)
+def _oracle_built():
+    """The C oracle is test infrastructure: build it if it is missing."""
+    from oracle import native
+    if not os.path.exists(native.LIB_PATH):
+        native.build()
+
+
+def activations(M: int, K: int, seed: int = 0, outlier_frac: float = 0.01,
+                outlier_scale: float = 50.0, dtype=np.float16) -> np.ndarray:
+    """X ~ N(0,1) [M, K] with ceil(1%) of channels (seeded choice) scaled x50."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    n_out = int(np.ceil(outlier_frac * K))
+    if n_out:
+        idx = torch.randperm(K, generator=torch.Generator().manual_seed(seed + 2))[:n_out]
+        x[:, idx] *= outlier_scale
+    return x.numpy().astype(dtype)
+
+
+def weights(N: int, K: int, seed: int = 1, std: float = 0.02, dtype=np.float16) -> np.ndarray:
+    """W ~ N(0, 0.02) [N, K]."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(N, K, generator=g) * std).numpy().astype(dtype)
+
+
+@pytest.fixture
+def gpu():
+    """cuda:0 after checking it is a gfx950 device with libdscq loaded."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a visible GPU")
+    import dscquant_amd
+    dscquant_amd._lib.require_gfx950(torch.device("cuda:0"))
+    return torch.device("cuda:0")

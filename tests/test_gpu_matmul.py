@@ -1,0 +1,154 @@
+"""GPU parity of the W4A4 GEMM (int8 MFMA path and skinny-M path).
+
+raw int32 accumulators are compared bit-exactly with the oracle's integer
+GEMM; the dequantized output is compared bit-exactly with the oracle's fp32
+epilogue narrowed to fp16 (same operation order, no fma), and additionally
+held to the max relative error 1e-3 against a float64 dequant of the same
+accumulators.  Operands are random bytes (every nibble value, both signs at
+the extremes) with random metadata, plus the end-to-end config data.
+"""
+import numpy as np
+import pytest
+import torch
+
+from dscquant_amd import w4a4
+from oracle import native
+from tests.conftest import activations, weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _operands(M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    MP, NP, KP = (M + 7) // 8 * 8, (N + 7) // 8 * 8, (K + 63) // 64 * 64
+    a = rng.integers(0, 256, size=(MP, KP // 2), dtype=np.uint8)
+    b = rng.integers(0, 256, size=(NP, KP // 2), dtype=np.uint8)
+    sx = (rng.random(MP).astype(np.float32) + 0.5) * 0.05
+    zx = rng.integers(0, 16, size=MP).astype(np.int32)
+    sw = (rng.random(NP).astype(np.float32) + 0.5) * 0.002
+    sums = rng.integers(-2000, 2000, size=NP).astype(np.int32)
+    return a, b, sx, zx, sw, sums
+
+
+def _oracle_raw(a, b, M, N):
+    KP = a.shape[1] * 2
+    if M * N * KP > 3e8:
+        return native.gemm_raw_blas(a, b, M, N)
+    return native.gemm_raw(a, b, M, N)
+
+
+def _dequant64(raw, sx, zx, sw, sums, bias, M, N):
+    corr = raw.astype(np.int64) + (8 - zx[:M, None].astype(np.int64)) * sums[None, :N]
+    out = corr.astype(np.float64) * sx[:M, None] * sw[None, :N]
+    if bias is not None:
+        out = out + bias[None, :N].astype(np.float64)
+    return out
+
+
+MM_CASES = [
+    # (M, N, K, bias, fp32, force_decode)
+    (1, 4096, 4096, False, False, False),
+    (4, 11008, 4096, False, False, False),
+    (7, 100, 64, True, False, False),
+    (8, 4096, 4096, False, False, False),
+    (16, 4096, 4096, True, False, False),
+    (16, 11008, 4096, False, False, False),
+    (16, 4096, 4096, False, False, True),
+    (33, 72, 192, True, True, False),
+    (64, 264, 320, False, False, True),
+    (128, 256, 4096, False, False, False),
+    (300, 520, 1088, True, False, False),
+    (512, 11008, 4096, False, False, False),
+    (512, 4096, 11008, False, False, False),
+    (1000, 1000, 1024, True, True, False),
+    (2048, 4096, 4096, False, False, False),
+]
+
+
+@pytest.mark.parametrize("M,N,K,use_bias,fp32,force_decode", MM_CASES,
+                         ids=[f"M{c[0]}-N{c[1]}-K{c[2]}-bias{int(c[3])}-fp32{int(c[4])}"
+                              f"-decode{int(c[5])}" for c in MM_CASES])
+def test_matmul_matches_oracle(gpu, M, N, K, use_bias, fp32, force_decode):
+    print(f"matmul case M{M} N{N} K{K} bias{use_bias} fp32{fp32} decode{force_decode}",
+          flush=True)
+    a, b, sx, zx, sw, sums = _operands(M, N, K, seed=M + 3 * N + 7 * K)
+    out_dtype = np.float32 if fp32 else np.float16
+    bias = (np.random.default_rng(K).standard_normal(N).astype(out_dtype)
+            if use_bias else None)
+    T = lambda v: torch.from_numpy(v).to(gpu)  # noqa: E731
+    tbias = T(bias) if use_bias else torch.empty(0, dtype=torch.float32 if fp32 else torch.float16,
+                                                 device=gpu)
+    out, raw = w4a4.matmul(T(a), T(b), T(sx), T(zx), T(sw), T(sums), tbias, M, N,
+                           fused=False, force_decode=force_decode, fp32=fp32)
+    out_f, raw_f = w4a4.matmul(T(a), T(b), T(sx), T(zx), T(sw), T(sums), tbias, M, N,
+                               fused=True, force_decode=force_decode, fp32=fp32)
+    torch.cuda.synchronize()
+    assert raw_f.numel() == 0
+    raw_ref = _oracle_raw(a, b, M, N)
+    np.testing.assert_array_equal(raw.cpu().numpy(), raw_ref)
+    out_ref = native.restore(raw_ref, sx, zx, sw, sums, bias, out_dtype=out_dtype)
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(got, out_ref)
+    np.testing.assert_array_equal(out_f.cpu().numpy(), got)
+    # north-star tolerance against a float64 dequant of the accumulators
+    exact = _dequant64(raw_ref, sx, zx, sw, sums, bias, M, N)
+    rel = np.abs(got.astype(np.float64) - exact) / np.maximum(np.abs(exact), 1e-30)
+    big = np.abs(exact) > 1e-2
+    assert rel[big].max() <= 1e-3
+
+
+def test_matmul_extreme_nibbles(gpu):
+    """All -8 x -8 and -8 x +7 at K = 4096: the largest |products| and sums."""
+    M, N, K = 40, 72, 4096
+    a = np.full((40, K // 2), 0x88, np.uint8)
+    b = np.full((72, K // 2), 0x88, np.uint8)
+    b[36:] = 0x77
+    T = lambda v: torch.from_numpy(v).to(gpu)  # noqa: E731
+    ones = lambda n: torch.ones(n, device=gpu)  # noqa: E731
+    zeros_i = lambda n: torch.full((n,), 8, dtype=torch.int32, device=gpu)  # noqa: E731
+    out, raw = w4a4.matmul(T(a), T(b), ones(40), zeros_i(40), ones(72),
+                           torch.zeros(72, dtype=torch.int32, device=gpu),
+                           torch.empty(0, dtype=torch.float32, device=gpu), M, N,
+                           fused=False, fp32=True)
+    r = raw.cpu().numpy()
+    assert (r[:, :36] == 64 * K).all() and (r[:, 36:] == -56 * K).all()
+
+
+def test_matmul_long_k(gpu):
+    """K beyond 65536 drains the scaled accumulator (worst-case magnitudes)."""
+    M, N, K = 16, 64, 139264
+    rng = np.random.default_rng(9)
+    a = np.full((16, K // 2), 0x88, np.uint8)
+    a[:, ::3] = rng.integers(0, 256, size=a[:, ::3].shape, dtype=np.uint8)
+    b = np.full((64, K // 2), 0x88, np.uint8)
+    T = lambda v: torch.from_numpy(v).to(gpu)  # noqa: E731
+    sx = np.ones(16, np.float32)
+    zx = np.full(16, 8, np.int32)
+    sw = np.ones(64, np.float32)
+    sums = np.zeros(64, np.int32)
+    out, raw = w4a4.matmul(T(a), T(b), T(sx), T(zx), T(sw), T(sums),
+                           torch.empty(0, dtype=torch.float32, device=gpu), M, N,
+                           fused=False, fp32=True)
+    np.testing.assert_array_equal(raw.cpu().numpy(), native.gemm_raw(a, b, M, N))
+
+
+@pytest.mark.parametrize("M,N,K,rot", [(16, 4096, 4096, 128), (2048, 4096, 4096, 128),
+                                       (5, 11008, 4096, 0), (512, 11008, 4096, 128)])
+def test_end_to_end_config_data(gpu, M, N, K, rot):
+    """quantize -> pack_weight -> matmul on the config distributions vs the oracle."""
+    print(f"end-to-end case M{M} N{N} K{K} rot{rot}", flush=True)
+    x = activations(M, K, seed=0)
+    w = weights(N, K, seed=1)
+    T = lambda v: torch.from_numpy(v).to(gpu)  # noqa: E731
+    pa, sx, zx = w4a4.quantize(T(x), 1.0, True, rot)
+    pw, sw, sums = w4a4.pack_weight(T(w), 1.0, rot)
+    out, raw = w4a4.matmul(pa, pw, sx, zx, sw, sums,
+                           torch.empty(0, dtype=torch.float16, device=gpu), M, N, fused=False)
+    pa_ref, sx_ref, zx_ref = native.quantize_rows(x.astype(np.float32), 1.0, rot)
+    pw_ref, sw_ref, sums_ref = native.pack_weight(w.astype(np.float32), 1.0, rot)
+    np.testing.assert_array_equal(pa.cpu().numpy(), pa_ref)
+    np.testing.assert_array_equal(pw.cpu().numpy(), pw_ref)
+    raw_ref = _oracle_raw(pa_ref, pw_ref, M, N)
+    np.testing.assert_array_equal(raw.cpu().numpy(), raw_ref)
+    out_ref = native.restore(raw_ref, sx_ref, zx_ref, sw_ref, sums_ref, None)
+    np.testing.assert_array_equal(out.cpu().numpy(), out_ref)

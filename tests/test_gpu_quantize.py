@@ -1,0 +1,199 @@
+"""GPU parity of the row-quantization kernels against the CPU oracle.
+
+Bit-exact: packed bytes, scales, zero-points, codes, weight sums.  Inputs are
+the seeded config distributions (N(0,1) activations with 1% outlier channels
+x50, N(0,0.02) weights) plus the edge cases the reference's rules single out:
+tiny / ragged K, padded rows, all-zero and constant rows, exact .5 ties (which
+drive the kernel's exact-division fallback), clip in {0.5, 0.75, 1}, fp16 and
+fp32 inputs, fused and two-pass forms, and rows long enough for the streaming
+kernel.
+"""
+import numpy as np
+import pytest
+import torch
+
+from dscquant_amd import w4a4
+from dscquant_amd.core import quantization as Q
+from oracle import native
+from tests.conftest import activations, weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _case_name(M, K, dtype, rot, clip, fused):
+    return f"M{M}-K{K}-{np.dtype(dtype).name}-rot{rot}-clip{clip}-{'fused' if fused else 'twopass'}"
+
+
+QUANT_CASES = [
+    # config shapes
+    (16, 4096, np.float16, 0, 1.0, True),
+    (16, 4096, np.float16, 128, 1.0, True),
+    (1, 4096, np.float16, 128, 1.0, True),
+    (4, 4096, np.float16, 0, 1.0, True),
+    (8, 4096, np.float16, 128, 1.0, True),
+    (2048, 4096, np.float16, 128, 1.0, True),
+    (2048, 4096, np.float16, 0, 1.0, True),
+    (512, 4096, np.float16, 0, 1.0, True),
+    (512, 11008, np.float16, 128, 1.0, True),
+    (64, 8192, np.float16, 128, 1.0, True),
+    (24, 28672, np.float16, 128, 1.0, True),
+    (3, 28672, np.float16, 0, 1.0, True),
+    # clip, dtype, two-pass
+    (100, 4096, np.float16, 128, 0.5, True),
+    (100, 4096, np.float16, 0, 0.75, False),
+    (37, 1024, np.float32, 128, 1.0, True),
+    (37, 1000, np.float32, 0, 0.9, False),
+    # ragged / tiny K (scalar load path), padded rows
+    (5, 100, np.float16, 0, 1.0, True),
+    (9, 1, np.float16, 0, 1.0, True),
+    (3, 63, np.float32, 0, 1.0, True),
+    (7, 64, np.float16, 0, 1.0, False),
+    (1200, 128, np.float16, 128, 1.0, True),
+    # streaming kernel (K beyond the register capacity)
+    (2, 40000, np.float16, 0, 1.0, True),
+    (3, 40064, np.float16, 128, 1.0, True),
+]
+
+
+@pytest.mark.parametrize("M,K,dtype,rot,clip,fused", QUANT_CASES,
+                         ids=[_case_name(*c) for c in QUANT_CASES])
+def test_quantize_matches_oracle(gpu, M, K, dtype, rot, clip, fused):
+    print(f"quantize case {_case_name(M, K, dtype, rot, clip, fused)}", flush=True)
+    x = activations(M, K, seed=M * 7 + K, dtype=dtype)
+    packed, scales, zeros = w4a4.quantize(torch.from_numpy(x).to(gpu), clip, fused, rot)
+    torch.cuda.synchronize()
+    p_ref, s_ref, z_ref = native.quantize_rows(x.astype(np.float32), clip, rot)
+    np.testing.assert_array_equal(scales.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(zeros.cpu().numpy(), z_ref)
+    np.testing.assert_array_equal(packed.cpu().numpy(), p_ref)
+
+
+def test_quantize_special_rows(gpu):
+    """All-zero, constant, all-positive and all-negative rows, one row each."""
+    K = 256
+    x = np.zeros((6, K), np.float32)
+    x[1] = 3.0
+    x[2] = np.linspace(0.1, 2.0, K)
+    x[3] = -np.linspace(0.1, 2.0, K)
+    x[4] = np.linspace(-1.0, 1.0, K)
+    x[5, 17] = -1e-3
+    for dtype in (np.float16, np.float32):
+        xd = x.astype(dtype)
+        for fused in (True, False):
+            got = w4a4.quantize(torch.from_numpy(xd).to(gpu), 1.0, fused)
+            ref = native.quantize_rows(xd.astype(np.float32), 1.0)
+            for g, r in zip(got, ref):
+                np.testing.assert_array_equal(g.cpu().numpy(), r)
+
+
+def _tie_rows(rows: int, K: int, zero: int = 0) -> np.ndarray:
+    """Rows whose x / scale + zero land exactly on j + .5.
+
+    lo = -zero/8 and hi = (15 - zero)/8 give scale = 1/8 exactly and the
+    zero-point `zero`; the other entries are (j + .5 - zero)/8.
+    """
+    rng = np.random.default_rng(5 + zero)
+    x = np.zeros((rows, K), np.float32)
+    for r in range(rows):
+        vals = (rng.integers(0, 15, size=K) + 0.5 - zero) / 8
+        i, k = rng.choice(K, size=2, replace=False)
+        vals[i] = (15 - zero) / 8
+        vals[k] = -zero / 8
+        x[r] = vals
+    return x
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_quantize_exact_ties_take_the_exact_path(gpu, dtype):
+    x = _tie_rows(64, 512).astype(dtype)
+    p, s, z = w4a4.quantize(torch.from_numpy(x).to(gpu), 1.0, True)
+    p_ref, s_ref, z_ref = native.quantize_rows(x.astype(np.float32), 1.0)
+    assert (s_ref[:64] == np.float32(0.125)).all()
+    np.testing.assert_array_equal(p.cpu().numpy(), p_ref)
+
+
+def test_quantize_ties_after_rotation(gpu):
+    """y = H x lands on exact ties: x = H y / 128 with y on the tie grid."""
+    K = 512
+    y = _tie_rows(32, K, zero=7)
+    from oracle import numpy_ref
+    H = numpy_ref.sylvester(128)
+    x = (y.reshape(32, K // 128, 128).astype(np.float64) @ H / 128).reshape(32, K)
+    x16 = x.astype(np.float16)
+    assert np.array_equal(x16.astype(np.float64), x)   # exactly representable
+    np.testing.assert_array_equal(native.fwht_rows(x16.astype(np.float32), 128), y)
+    p, s, z = w4a4.quantize(torch.from_numpy(x16).to(gpu), 1.0, True, 128)
+    p_ref, s_ref, z_ref = native.quantize_rows(x16.astype(np.float32), 1.0, 128)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(p.cpu().numpy(), p_ref)
+
+
+WEIGHT_CASES = [
+    (4096, 4096, np.float16, 0, 1.0),
+    (4096, 4096, np.float16, 128, 1.0),
+    (11008, 4096, np.float16, 128, 1.0),
+    (4096, 11008, np.float16, 128, 1.0),
+    (100, 1000, np.float32, 0, 0.8),
+    (20, 200, np.float16, 0, 1.0),
+    (1, 64, np.float16, 0, 1.0),
+    (13, 40064, np.float16, 128, 1.0),
+]
+
+
+@pytest.mark.parametrize("N,K,dtype,rot,clip", WEIGHT_CASES,
+                         ids=[f"N{c[0]}-K{c[1]}-{np.dtype(c[2]).name}-rot{c[3]}-clip{c[4]}"
+                              for c in WEIGHT_CASES])
+def test_pack_weight_matches_oracle(gpu, N, K, dtype, rot, clip):
+    print(f"pack_weight case N{N} K{K} rot{rot}", flush=True)
+    w = weights(N, K, seed=N + K, dtype=dtype)
+    packed, sw, sums, codes = w4a4.pack_weight(torch.from_numpy(w).to(gpu), clip, rot,
+                                               return_codes=True)
+    p_ref, sw_ref, sums_ref = native.pack_weight(w.astype(np.float32), clip, rot)
+    np.testing.assert_array_equal(sw.cpu().numpy(), sw_ref)
+    np.testing.assert_array_equal(sums.cpu().numpy(), sums_ref)
+    np.testing.assert_array_equal(packed.cpu().numpy(), p_ref)
+    KP = p_ref.shape[1] * 2
+    np.testing.assert_array_equal(codes.cpu().numpy(), native.unpack_int4(p_ref, KP))
+
+
+# ------------------------------------------------------- reference-named API
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_activation_codes_api(gpu, bits):
+    x = activations(3 * 40, 384, seed=bits).reshape(3, 40, 384)
+    code, scale, zero = Q.activation_codes(torch.from_numpy(x).to(gpu), bits, 0.75)
+    c_ref, s_ref, z_ref = native.activation_codes(x.reshape(120, 384).astype(np.float32), bits, 0.75)
+    assert code.shape == (3, 40, 384) and scale.shape == (3, 40, 1) and zero.shape == (3, 40, 1)
+    assert code.dtype == torch.float32
+    np.testing.assert_array_equal(code.cpu().numpy().reshape(120, 384), c_ref.astype(np.float32))
+    np.testing.assert_array_equal(scale.cpu().numpy().reshape(120), s_ref)
+    np.testing.assert_array_equal(zero.cpu().numpy().reshape(120), z_ref)
+    # quantize_activation keeps the input dtype: ((code - zero) * scale).to(x.dtype)
+    xa = Q.quantize_activation(torch.from_numpy(x).to(gpu), bits, 0.75)
+    assert xa.dtype == torch.float16
+    ref = ((c_ref.astype(np.float32) - z_ref[:, None]) * s_ref[:, None]).astype(np.float16)
+    np.testing.assert_array_equal(xa.cpu().numpy().reshape(120, 384), ref)
+
+
+@pytest.mark.parametrize("bits", [3, 4, 8])
+def test_weight_codes_api(gpu, bits):
+    w = weights(72, 520, seed=bits)
+    code, scale = Q.weight_codes(torch.from_numpy(w).to(gpu), bits, 0.9)
+    c_ref, s_ref = native.weight_codes(w.astype(np.float32), bits, 0.9)
+    assert code.shape == (72, 520) and scale.shape == (72, 1)
+    np.testing.assert_array_equal(code.cpu().numpy(), c_ref.astype(np.float32))
+    np.testing.assert_array_equal(scale.cpu().numpy()[:, 0], s_ref)
+    wq = Q.quantize_weight(torch.from_numpy(w).to(gpu), bits, 0.9)
+    np.testing.assert_array_equal(
+        wq.cpu().numpy(), (c_ref.astype(np.float32) * s_ref[:, None]).astype(np.float16))
+
+
+def test_pack_unpack_int4_api(gpu):
+    rng = np.random.default_rng(0)
+    c = rng.integers(-8, 8, size=(33, 77)).astype(np.int8)
+    p = Q.pack_int4(torch.from_numpy(c).to(gpu))
+    np.testing.assert_array_equal(p.cpu().numpy(), native.pack_int4(c))
+    u = Q.unpack_int4(p, 77)
+    np.testing.assert_array_equal(u.cpu().numpy(), c)
+    with pytest.raises(ValueError, match="Signed INT4 code out of range."):
+        Q.pack_int4(torch.full((2, 2), 8, dtype=torch.int8, device=gpu))

@@ -28,6 +28,9 @@
 // LDS stages double-buffer the slices: global loads for slice k+1 are in
 // flight while slice k feeds the matrix cores; one barrier per slice.
 
+#include <cstdlib>
+#include <cstring>
+
 #include "../../include/dscq.h"
 #include "common.h"
 
@@ -243,8 +246,29 @@ int launch_cfg(GemmArgs g, hipStream_t stream) {
   return launch_status("w4a4_gemm_kernel");
 }
 
+// DSCQ_GEMM_TILE=<BM>x<BN>[w8] pins the tile shape (tuning sweeps only).
+template <typename OutT>
+int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
+  static const char* env = getenv("DSCQ_GEMM_TILE");
+  *handled = 1;
+  if (env && g.KP <= 65536) {
+    if (!strcmp(env, "128x256")) return launch_cfg<OutT, 128, 256, 2, 2, false>(g, stream);
+    if (!strcmp(env, "128x128")) return launch_cfg<OutT, 128, 128, 2, 2, false>(g, stream);
+    if (!strcmp(env, "256x128")) return launch_cfg<OutT, 256, 128, 2, 2, false>(g, stream);
+    if (!strcmp(env, "256x256")) return launch_cfg<OutT, 256, 256, 2, 2, false>(g, stream);
+    if (!strcmp(env, "128x256w8")) return launch_cfg<OutT, 128, 256, 2, 4, false>(g, stream);
+    if (!strcmp(env, "256x128w8")) return launch_cfg<OutT, 256, 128, 4, 2, false>(g, stream);
+    if (!strcmp(env, "64x128")) return launch_cfg<OutT, 64, 128, 2, 2, false>(g, stream);
+  }
+  *handled = 0;
+  return 0;
+}
+
 template <typename OutT>
 int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
+  int handled = 0;
+  const int rc = tile_override<OutT>(g, stream, &handled);
+  if (handled) return rc;
   if (g.KP > 65536) return launch_cfg<OutT, 64, 64, 2, 2, true>(g, stream);
   if (decode || g.M <= 32) return launch_cfg<OutT, 32, 128, 1, 4, false>(g, stream);
   const int64_t big_tiles = ((g.M + 127) / 128) * ((g.N + 255) / 256);

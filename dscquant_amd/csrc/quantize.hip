@@ -57,53 +57,82 @@ struct RowArgs {
 };
 
 // ------------------------------------------------------------------ loading
-
-__device__ __forceinline__ void cvt8(const uint4 r, float v[8]) {
-  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = __half2float(__ushort_as_half((unsigned short)(w[i] & 0xFFFFu)));
-    v[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(w[i] >> 16)));
-  }
-}
+// Loads are unconditional: an out-of-range chunk reads element 0 of its row
+// (always valid) and is zeroed afterwards, so every 16-byte load of a lane
+// is in flight at once instead of each waiting inside its own branch.
+// Zero is a neutral placeholder: it never moves min(x, 0) / max(x, 0) or
+// max|w|, and it quantizes to the row's zero-point (activations) or to 0
+// (weights) -- exactly the padding the reference writes.
 
 template <typename T>
-__device__ __forceinline__ void load_chunk(const T* row, int64_t e0, int64_t K,
-                                           bool vec, float v[8]);
+struct Raw;
+template <>
+struct Raw<__half> {
+  uint4 w;
+};
+template <>
+struct Raw<float> {
+  uint4 w0, w1;
+};
+
+template <typename T>
+__device__ __forceinline__ Raw<T> load_raw(const T* row, int64_t e0, bool ok);
 
 template <>
-__device__ __forceinline__ void load_chunk<__half>(const __half* row, int64_t e0,
-                                                   int64_t K, bool vec,
-                                                   float v[8]) {
-  if (vec) {
-    if (e0 < K) {
-      cvt8(*reinterpret_cast<const uint4*>(row + e0), v);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (e0 + i < K) ? __half2float(row[e0 + i]) : 0.0f;
-  }
+__device__ __forceinline__ Raw<__half> load_raw<__half>(const __half* row, int64_t e0,
+                                                        bool ok) {
+  Raw<__half> r;
+  r.w = *reinterpret_cast<const uint4*>(row + (ok ? e0 : 0));
+  return r;
 }
 
 template <>
-__device__ __forceinline__ void load_chunk<float>(const float* row, int64_t e0,
-                                                  int64_t K, bool vec, float v[8]) {
-  if (vec) {
-    if (e0 < K) {
-      const float4 a = *reinterpret_cast<const float4*>(row + e0);
-      const float4 b = *reinterpret_cast<const float4*>(row + e0 + 4);
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
+__device__ __forceinline__ Raw<float> load_raw<float>(const float* row, int64_t e0,
+                                                      bool ok) {
+  Raw<float> r;
+  const float* p = row + (ok ? e0 : 0);
+  r.w0 = *reinterpret_cast<const uint4*>(p);
+  r.w1 = *reinterpret_cast<const uint4*>(p + 4);
+  return r;
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return __half2float(__ushort_as_half((unsigned short)bits16));
+}
+
+// Zero the values of a chunk that was loaded from the placeholder address.
+template <typename T>
+__device__ __forceinline__ void mask_f32(bool ok, float v[8]) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-    }
-  } else {
+  for (int i = 0; i < 8; ++i) v[i] = ok ? v[i] : 0.0f;
+}
+
+__device__ __forceinline__ void to_f32(const Raw<__half>& r, float v[8]) {
+  const uint32_t w[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (e0 + i < K) ? row[e0 + i] : 0.0f;
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = h2f(w[i] & 0xFFFFu);
+    v[2 * i + 1] = h2f(w[i] >> 16);
+  }
+}
+
+__device__ __forceinline__ void to_f32(const Raw<float>& r, float v[8]) {
+  v[0] = __uint_as_float(r.w0.x); v[1] = __uint_as_float(r.w0.y);
+  v[2] = __uint_as_float(r.w0.z); v[3] = __uint_as_float(r.w0.w);
+  v[4] = __uint_as_float(r.w1.x); v[5] = __uint_as_float(r.w1.y);
+  v[6] = __uint_as_float(r.w1.z); v[7] = __uint_as_float(r.w1.w);
+}
+
+// Element-wise form for rows that are not 16-byte aligned or whose K is not a
+// multiple of 8 (streaming kernel only).
+template <typename T>
+__device__ __forceinline__ void load_scalar(const T* row, int64_t e0, int64_t K, bool ok,
+                                            float v[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool in = ok && (e0 + i < K);
+    const float f = (float)row[in ? e0 + i : 0];
+    v[i] = in ? f : 0.0f;
   }
 }
 
@@ -286,23 +315,28 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
   const int quad = wave_in_row * 16 + (lane >> 2);
   const int r = lane & 3;
   const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.K;
-  const bool vec = a.vec != 0;
 
-  float v[ITERS][4][8];
+  // Rows of this kernel are 16-byte aligned with K % 8 == 0 (see row_quant).
+  Raw<T> raw[ITERS][4];
+  bool ok[ITERS][4];
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     const int b = quad + it * NQ;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
-      if (real && b < a.nblk) {
-        load_chunk<T>(xrow, e0, a.K, vec, v[it][j]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[it][j][i] = 0.0f;
-      }
+      ok[it][j] = real && b < a.nblk && e0 < a.K;
+      raw[it][j] = load_raw<T>(xrow, e0, ok[it][j]);
     }
   }
+  float v[ITERS][4][8];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      to_f32(raw[it][j], v[it][j]);
+      mask_f32<T>(ok[it][j], v[it][j]);
+    }
 
   if (ROT) {
 #pragma unroll
@@ -406,15 +440,24 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
 template <typename T, bool ROT, int MODE>
 __device__ __forceinline__ void load_block(const RowArgs& a, const T* xrow, bool real,
                                            int b, int r, float c[4][8]) {
+  if (a.vec) {
+    Raw<T> raw[4];
+    bool ok[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
-    if (real && b < a.nblk) {
-      load_chunk<T>(xrow, e0, a.K, a.vec != 0, c[j]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) c[j][i] = 0.0f;
+    for (int j = 0; j < 4; ++j) {
+      const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
+      ok[j] = real && b < a.nblk && e0 < a.K;
+      raw[j] = load_raw<T>(xrow, e0, ok[j]);
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      to_f32(raw[j], c[j]);
+      mask_f32<T>(ok[j], c[j]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      load_scalar<T>(xrow, (int64_t)b * 128 + j * 32 + r * 8, a.K, real && b < a.nblk, c[j]);
   }
   if (ROT) {
 #pragma unroll
@@ -640,6 +683,7 @@ int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float 
           ((K * esize) % 16 == 0);
   int wpr, iters;
   pick_shape(MP, a.nblk, &wpr, &iters);
+  if (!a.vec) wpr = iters = 0;  // element-wise loads: streaming kernel only
   const bool rot = rotate_block != 0;
 #define DSCQ_T(T)                                                                    \
   if (rot)                                                                           \

@@ -30,6 +30,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "../../include/dscq.h"
 #include "common.h"
@@ -69,8 +70,13 @@ __device__ __forceinline__ v4i unpack8(uint32_t w0, uint32_t w1) {
 
 template <typename OutT>
 __device__ __forceinline__ OutT to_out(float v);
+// The reference rounds the fp32 result, then narrows it to fp16 (two
+// roundings).  Left alone, the compiler folds a preceding fp32 multiply / add
+// into the narrowing (v_fma_mixlo_f16: one rounding), which differs on exact
+// fp16 ties; the empty asm pins the fp32 value first.
 template <>
 __device__ __forceinline__ __half to_out<__half>(float v) {
+  asm("" : "+v"(v));
   return __float2half_rn(v);
 }
 template <>
@@ -205,33 +211,339 @@ __global__ __launch_bounds__(64 * WM * WN) void w4a4_gemm_kernel(GemmArgs g) {
   }
 
   // ---- epilogue: D[i][j] of a 32x32 tile sits in lane (j % 32) + 32 * ((i / 4) % 2),
-  // register (i % 4) + 4 * (i / 8).
+  // register (i % 4) + 4 * (i / 8).  All row / column metadata is fetched
+  // before any of it is used, so the loads overlap.
   OutT* out = static_cast<OutT*>(g.out);
   const OutT* bias = static_cast<const OutT*>(g.bias);
+  float sxr[FM][16];
+  int32_t zr[FM][16];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t row = min(m0 + wm * TM + i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2),
+                              g.arows - 1);
+      sxr[i][v] = g.sx[row];
+      zr[i][v] = 8 - g.zx[row];
+    }
+  float swc[FN], bc[FN];
+  int32_t sumc[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t col = n0 + wn * TN + j * 32 + (lane & 31);
+    const int64_t colc = col < g.N ? col : 0;
+    swc[j] = g.sw[colc];
+    sumc[j] = g.sums[colc];
+    bc[j] = bias ? (float)bias[colc] : 0.0f;
+  }
+  // The raw-accumulator mode is a separate uniform path so that store data
+  // registers of one mode are never recycled under the other's stores.
+  auto store_all = [&](auto with_raw) {
+  constexpr bool WITH_RAW = decltype(with_raw)::value;
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int64_t col = n0 + wn * TN + j * 32 + (lane & 31);
     const bool col_ok = col < g.N;
-    const float swc = col_ok ? g.sw[col] : 0.0f;
-    const int32_t sumc = col_ok ? g.sums[col] : 0;
-    const float bc = (col_ok && bias) ? (float)bias[col] : 0.0f;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int64_t row = m0 + wm * TM + i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
-        if (!col_ok || row >= g.M) continue;
         int32_t r = acc[i][j][v] >> 8;
         if (HUGE) r += tot[HUGE ? i : 0][HUGE ? j : 0][v];
-        const int32_t corrected = r + (8 - g.zx[row]) * sumc;
-        float res = (float)corrected * g.sx[row];
-        res = res * swc;
-        if (bias) res = res + bc;
-        out[row * g.N + col] = to_out<OutT>(res);
-        if (g.raw) g.raw[row * g.N + col] = r;
+        const int32_t corrected = r + zr[i][v] * sumc[j];
+        float res = (float)corrected * sxr[i][v];
+        res = res * swc[j];
+        if (bias) res = res + bc[j];
+        if (col_ok && row < g.M) {
+          out[row * g.N + col] = to_out<OutT>(res);
+          if (WITH_RAW) g.raw[row * g.N + col] = r;
+        }
       }
     }
   }
+  };
+  if (g.raw)
+    store_all(std::true_type{});
+  else
+    store_all(std::false_type{});
+}
+
+// ------------------------------------------------------ pipelined kernel
+// BM x BN output tile, WM x WN waves, each wave a (BM/WM) x (BN/WN) block of
+// 32 x 32 MFMA tiles.  LDS holds a K slice (64 bytes = 128 nibbles per row)
+// row-major, A rows then B rows, with the four 16-byte units of a row
+// XOR-swizzled by bits 2-3 of the row so that the 16-byte fragment reads of
+// 16 consecutive lanes (16 consecutive rows) hit distinct banks.  Lane l of a
+// fragment reads row l % 32, unit 2q + l / 32 (q = 0, 1): the low 8 bytes
+// feed MFMA step 2q, the high 8 bytes step 2q + 1 -- the same assignment for
+// A and B, so every product pairs equal k.
+//
+// Pipeline (one barrier per slice): global loads run two slices ahead into
+// registers; slice s + 1 is written to the idle LDS buffer while slice s
+// (already in registers) feeds the matrix cores; after the barrier the next
+// slice's fragments are read back while the last MFMA step of slice s runs.
+// Each step interleaves its MFMAs with the nibble unpack of the next step's
+// fragments.  The tile's row scales / zero-points are staged in LDS once.
+// The epilogue writes each wave's fp16 (or fp32) tile to LDS and stores it
+// row-contiguously in 16-byte pieces (N % 8 == 0, 16-byte aligned output).
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <typename OutT, int BM, int BN, int WM, int WN, int MINB, bool KTAIL, bool BIAS>
+__global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(GemmArgs g) {
+  constexpr int THREADS = 64 * WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32, NF = FM + FN;
+  constexpr int ROWS = BM + BN;
+  constexpr int STAGE = ROWS * 64;
+  constexpr int LOADS = ROWS * 4 / THREADS;  // 16-byte pieces per thread per slice
+  static_assert(ROWS * 4 % THREADS == 0 && THREADS / 4 % 16 == 0, "load split");
+  constexpr int ROWB = TN * (int)sizeof(OutT) + 16;  // staged output row, padded
+  constexpr int OUT_LDS = WM * WN * TM * ROWB;
+  constexpr int MAIN_LDS = 2 * STAGE > OUT_LDS ? 2 * STAGE : OUT_LDS;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[MAIN_LDS + BM * 8];
+  float* const lds_sx = reinterpret_cast<float*>(smem + MAIN_LDS);
+  int32_t* const lds_z = reinterpret_cast<int32_t*>(smem + MAIN_LDS + BM * 4);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int tile_m = blockIdx.x / g.tiles_n;
+  const int tile_n = blockIdx.x % g.tiles_n;
+  const int64_t m0 = (int64_t)tile_m * BM;
+  const int64_t n0 = (int64_t)tile_n * BN;
+  const int64_t KB = g.KP / 2;
+  const int nslices = (int)((KB + 63) / 64);
+
+  // Global pieces of this thread: logical unit u = tid % 4 of rows
+  // tid / 4 + (THREADS / 4) i.  Rows past MP / NP are clamped (never stored).
+  const int u = tid & 3;
+  const uint8_t* src[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int R = (tid >> 2) + (THREADS / 4) * i;
+    if (R < BM) {
+      const int64_t row = min(m0 + R, g.arows - 1);
+      src[i] = g.a + row * KB + u * 16;
+    } else {
+      const int64_t row = min(n0 + (R - BM), g.brows - 1);
+      src[i] = g.b + row * KB + u * 16;
+    }
+  }
+  // (R >> 2) & 3 == (tid >> 4) & 3 because THREADS / 4 is a multiple of 16.
+  const int wr_off = (tid >> 2) * 64 + 16 * (u ^ ((tid >> 4) & 3));
+
+  auto gload = [&](uint4 (&st)[LOADS], int slice) {
+    const int sl = min(slice, nslices - 1);
+    const int64_t kb = (int64_t)sl * 64;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      uint4 v = *reinterpret_cast<const uint4*>(src[i] + kb);
+      if (KTAIL && kb + u * 16 >= KB) v = make_uint4(0u, 0u, 0u, 0u);
+      st[i] = v;
+    }
+  };
+  auto lstore = [&](const uint4 (&st)[LOADS], int buf) {
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i)
+      *reinterpret_cast<uint4*>(smem + buf * STAGE + wr_off + i * (THREADS / 4) * 64) = st[i];
+  };
+
+  // Fragment read offsets (bytes within a stage) for q = 0, 1.
+  const int fr_row = lane & 31;
+  const int fr_sw = (lane >> 2) & 3;
+  int rd_off[NF][2];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int R = f < FM ? (wm * TM + f * 32 + fr_row) : (BM + wn * TN + (f - FM) * 32 + fr_row);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) rd_off[f][q] = R * 64 + 16 * ((2 * q + (lane >> 5)) ^ fr_sw);
+  }
+  uint4 P[2][NF];
+  auto lread = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        P[q][f] = *reinterpret_cast<const uint4*>(smem + buf * STAGE + rd_off[f][q]);
+  };
+
+  v16i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v16i{0};
+
+  v4i U0[NF], U1[NF];
+  // step t of a slice uses P[t / 2] dwords (2 * (t % 2), +1).
+  auto unpack_step = [&](v4i (&U)[NF], int t) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint4 w = P[t >> 1][f];
+      U[f] = (t & 1) ? unpack8(w.z, w.w) : unpack8(w.x, w.y);
+    }
+  };
+  auto mfma_step = [&](const v4i (&U)[NF]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(U[i], U[FM + j], acc[i][j], 0, 0, 0);
+  };
+  // Pins the instruction mix of one step: MFMA, a share of the VALU work,
+  // MFMA, ...; the closing sched_barrier keeps every step's memory
+  // operations inside it.
+  constexpr int VPM = (6 * NF + FM * FN - 1) / (FM * FN);  // unpack VALU per MFMA
+  auto interleave = [&]() {
+#pragma unroll
+    for (int k = 0; k < FM * FN; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  uint4 G0[LOADS], G1[LOADS];
+  gload(G0, 0);
+  gload(G1, 1);
+  // Row metadata of the tile, once per workgroup (after the slice loads, so
+  // the first slice is not queued behind it).
+  if (tid < BM) {
+    const int64_t row = min(m0 + tid, g.arows - 1);
+    lds_sx[tid] = g.sx[row];
+    lds_z[tid] = 8 - g.zx[row];
+  }
+  lstore(G0, 0);
+  lds_barrier();
+  lread(0);
+  unpack_step(U0, 0);
+
+  // st_next holds slice s + 1 (loaded during slice s - 1); st_free held
+  // slice s, already in LDS, and now receives slice s + 2.
+  auto slice = [&](int s, uint4 (&st_next)[LOADS], uint4 (&st_free)[LOADS]) {
+    const int nbuf = (s + 1) & 1;
+    mfma_step(U0);
+    unpack_step(U1, 1);
+    gload(st_free, s + 2);
+    interleave();
+    mfma_step(U1);
+    unpack_step(U0, 2);
+    interleave();
+    mfma_step(U0);
+    unpack_step(U1, 3);
+    lstore(st_next, nbuf);
+    interleave();
+    lds_barrier();
+    lread(nbuf);
+    mfma_step(U1);
+    unpack_step(U0, 0);
+    interleave();
+  };
+  // Slice s + 1 sits in G1 when s is even, in G0 when s is odd.
+  int s = 0;
+  for (; s + 1 < nslices; s += 2) {
+    slice(s, G1, G0);
+    slice(s + 1, G0, G1);
+  }
+  if (s < nslices) slice(s, G1, G0);
+
+  // ---- epilogue.  D[i][j] of a 32x32 tile sits in lane (j % 32) + 32 * ((i / 4) % 2),
+  // register (i % 4) + 4 * (i / 8).  Operation order of kernel/w4a4.cu:74-77;
+  // |8 - zx| <= 8 and |sums| < 2^23, so the 24-bit multiply is exact.
+  const OutT* bias = static_cast<const OutT*>(g.bias);
+  float swc[FN], bc[FN];
+  int32_t sumc[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t col = n0 + wn * TN + j * 32 + (lane & 31);
+    const int64_t colc = col < g.N ? col : 0;
+    swc[j] = g.sw[colc];
+    sumc[j] = g.sums[colc];
+    bc[j] = BIAS ? (float)bias[colc] : 0.0f;
+  }
+  lds_barrier();  // every wave is done with the K slices; row metadata visible
+  auto value = [&](int i, int j, int v) {
+    const int r = wm * TM + i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+    const int32_t corrected = (acc[i][j][v] >> 8) + __mul24(lds_z[r], sumc[j]);
+    float res = (float)corrected * lds_sx[r];
+    res = res * swc[j];
+    if (BIAS) res = res + bc[j];
+    return res;
+  };
+  if (g.raw) {
+    // Raw-accumulator mode (the reference's unfused matmul): plain stores.
+    OutT* out = static_cast<OutT*>(g.out);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t row = m0 + wm * TM + i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+          const int64_t col = n0 + wn * TN + j * 32 + (lane & 31);
+          if (row < g.M && col < g.N) {
+            g.raw[row * g.N + col] = acc[i][j][v] >> 8;
+            out[row * g.N + col] = to_out<OutT>(value(i, j, v));
+          }
+        }
+    return;
+  }
+  // Stage the wave's TM x TN tile in LDS, then write it out row-contiguously.
+  uint8_t* tile = smem + wave * TM * ROWB;
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+        const int c = j * 32 + (lane & 31);
+        *reinterpret_cast<OutT*>(tile + r * ROWB + c * (int)sizeof(OutT)) =
+            to_out<OutT>(value(i, j, v));
+      }
+  constexpr int CHUNKS = TN * (int)sizeof(OutT) / 16;  // 16-byte pieces per row
+  constexpr int RPI = 64 / CHUNKS;                      // rows per wave instruction
+  OutT* out = static_cast<OutT*>(g.out);
+  const int cpos = lane % CHUNKS;
+  const int64_t col0 = n0 + wn * TN + cpos * (16 / (int)sizeof(OutT));
+#pragma unroll
+  for (int k = 0; k < TM / RPI; ++k) {
+    const int r = k * RPI + lane / CHUNKS;
+    const uint4 w = *reinterpret_cast<const uint4*>(tile + r * ROWB + cpos * 16);
+    const int64_t row = m0 + wm * TM + r;
+    if (row < g.M && col0 < g.N) *reinterpret_cast<uint4*>(out + row * g.N + col0) = w;
+  }
+}
+
+template <typename OutT, int BM, int BN, int WM, int WN, int MINB>
+int launch_pipe_cfg(GemmArgs g, hipStream_t stream) {
+  g.tiles_n = (int)((g.N + BN - 1) / BN);
+  const int64_t nblocks = ((g.M + BM - 1) / BM) * g.tiles_n;
+  if (nblocks > 0x7FFFFFFF) return fail("matmul: grid too large");
+  const bool ktail = (g.KP / 2) % 64 != 0;
+  const dim3 grid((unsigned)nblocks), block(64 * WM * WN);
+#define DSCQ_PIPE(KT, BI)                                                                  \
+  hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<OutT, BM, BN, WM, WN, MINB, KT, BI>), grid, block, \
+                     0, stream, g)
+  if (g.bias) {
+    if (ktail) DSCQ_PIPE(true, true); else DSCQ_PIPE(false, true);
+  } else {
+    if (ktail) DSCQ_PIPE(true, false); else DSCQ_PIPE(false, false);
+  }
+#undef DSCQ_PIPE
+  return launch_status("w4a4_gemm_pipe_kernel");
+}
+
+// 256 x 128 tiles with two waves per SIMD when they fill the chip, else
+// 128 x 128 tiles (two workgroups per CU).
+template <typename OutT>
+int launch_pipe(GemmArgs g, hipStream_t stream) {
+  const int64_t big = ((g.M + 255) / 256) * ((g.N + 127) / 128);
+  if (big >= 256) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
+  return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
 }
 
 template <typename OutT, int BM, int BN, int WM, int WN, bool HUGE>
@@ -259,6 +571,10 @@ int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
     if (!strcmp(env, "128x256w8")) return launch_cfg<OutT, 128, 256, 2, 4, false>(g, stream);
     if (!strcmp(env, "256x128w8")) return launch_cfg<OutT, 256, 128, 4, 2, false>(g, stream);
     if (!strcmp(env, "64x128")) return launch_cfg<OutT, 64, 128, 2, 2, false>(g, stream);
+    if (!strcmp(env, "pipe")) return launch_pipe<OutT>(g, stream);
+    if (!strcmp(env, "pipe128x256")) return launch_pipe_cfg<OutT, 128, 256, 2, 2, 1>(g, stream);
+    if (!strcmp(env, "pipe128")) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
+    if (!strcmp(env, "pipe256x128w8")) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
   }
   *handled = 0;
   return 0;
@@ -271,6 +587,8 @@ int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
   if (handled) return rc;
   if (g.KP > 65536) return launch_cfg<OutT, 64, 64, 2, 2, true>(g, stream);
   if (decode || g.M <= 32) return launch_cfg<OutT, 32, 128, 1, 4, false>(g, stream);
+  const bool aligned16 = (reinterpret_cast<uintptr_t>(g.out) & 15) == 0;
+  if (g.N % 8 == 0 && aligned16 && g.M >= 64) return launch_pipe<OutT>(g, stream);
   const int64_t big_tiles = ((g.M + 127) / 128) * ((g.N + 255) / 256);
   if (big_tiles >= 192) return launch_cfg<OutT, 128, 256, 2, 2, false>(g, stream);
   return launch_cfg<OutT, 128, 128, 2, 2, false>(g, stream);

@@ -23,14 +23,19 @@
 //
 // Exact division at bandwidth.  The reference computes
 // code = clamp(round_half_even(fl(fl(x / s) + z))).  Per element we use
-// t = fma(x, y, z) with y = fl(1 / s) computed once per row.  Writing
-// Q = x / s, |x*y - Q| <= 2^-24 |Q| and |fl(Q) - Q| <= 2^-24 |Q|, and both
-// sums are rounded once more, so |t - fl(fl(Q) + z)| <= 2^-23 |Q| + ulp(T)
-// with T = |Q| + qmax.  If t lies further than delta = (|Q|max + 16) * 2^-21
-// (a 2x margin over that bound) from every half-integer, t and the exact
-// value round to the same integer; a lane that sees any element closer than
-// that recomputes all its elements with IEEE division (rare: ~1e-4 of lanes).
+// t = fma(x, y, z) with y = rcp(s) (relative error <= 2^-23) computed once per
+// row.  Writing Q = x / s, the exact x*y is within 2^-23 |Q| of Q and fl(Q)
+// within 2^-24 |Q|; each side is rounded once more to T-sized numbers
+// (T <= |Q| + qmax, ulp(T) <= 2^-23 T), so |t - fl(fl(Q) + z)| <=
+// 2^-23 (2.5 |Q| + qmax).  If t lies further than
+// delta = (|Q|max + qmax + 1) * 2^-21 (at least 1.6x that bound) from every
+// half-integer, t and the exact value round to the same integer; a lane that
+// sees any element closer than that recomputes all its elements with IEEE
+// division (rare: ~1e-4 of lanes).
 // Clamping commutes with rounding because the bounds are integers.
+
+#include <cstdio>
+#include <cstdlib>
 
 #include "../../include/dscq.h"
 #include "common.h"
@@ -240,9 +245,10 @@ __device__ __forceinline__ RowScale row_scale(float mn, float mx, float clip,
     const float lo = mn * clip, hi = mx * clip;
     rs.scale = fmaxf((hi - lo) / qmax, 1e-8f);
     rs.zf = __builtin_amdgcn_fmed3f(__builtin_rintf(-lo / rs.scale), 0.0f, qmax);
-    rs.y = 1.0f / rs.scale;
+    // Only the fast path uses y; a 1-ulp reciprocal is inside its margin.
+    rs.y = __builtin_amdgcn_rcpf(rs.scale);
     const float qbound = fmaxf(mx, -mn) / rs.scale;
-    rs.thr = 0.5f - (qbound + 16.0f) * 0x1p-21f;
+    rs.thr = 0.5f - (qbound + qmax + 1.0f) * 0x1p-21f;
   } else {
     // core/quantization.py:9 (amax * clip / bound, then the 1e-8 floor).
     rs.scale = fmaxf(mx * clip / qmax, 1e-8f);
@@ -286,6 +292,102 @@ __device__ __forceinline__ void store_chunk(const RowArgs& a, int64_t row,
   }
 }
 
+// --------------------------------------------------------- register kernel
+
+// First butterfly stage straight from a dword holding two fp16 values:
+// y0 = lo + hi, y1 = lo - hi, each a single IEEE fp32 rounding of the exact
+// result (v_fma_mix widens the fp16 operands exactly), so the fp16 -> fp32
+// conversion costs nothing.
+__device__ __forceinline__ void bfly_f16x2(uint32_t w, float& y0, float& y1) {
+  asm("v_fma_mix_f32 %0, %1, 1.0, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(y0) : "v"(w));
+  asm("v_fma_mix_f32 %0, %1, -1.0, %1 op_sel:[1,0,0] op_sel_hi:[1,0,1]" : "=v"(y1) : "v"(w));
+}
+
+// Stages for index bits 1 and 2 of one chunk (bit 0 already applied).
+__device__ __forceinline__ void fwht_chunk_tail(float v[8]) {
+#pragma unroll
+  for (int h = 2; h < 8; h <<= 1)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (!(i & h)) {
+        const float u = v[i], w = v[i + h];
+        v[i] = u + w;
+        v[i + h] = u - w;
+      }
+}
+
+// Cross-lane stages of the register kernel, one instruction per element:
+// v_fmac_f32_dpp computes own + sgn * partner, partner read across the quad
+// by DPP.  For the pair (lo, hi) the lane holding lo (sgn = +1) gets lo + hi,
+// the lane holding hi (sgn = -1) gets hi - lo = -(lo - hi): exactly the
+// negated butterfly output, since round-to-nearest is symmetric.  Each stage
+// thus leaves a known per-lane sign, tracked by the caller (lanes r = 1 and
+// r = 2 of a quad end up holding -y).  The leading s_nop covers the
+// two-wait-state gap gfx9 requires between a VALU write and a DPP read.
+#define DSCQ_FMAC_DPP8(PERM)                                                              \
+  asm("s_nop 1\n\t"                                                                       \
+      "v_fmac_f32_dpp %0, %0, %8 quad_perm:" PERM " row_mask:0xf bank_mask:0xf\n\t"       \
+      "v_fmac_f32_dpp %1, %1, %8 quad_perm:" PERM " row_mask:0xf bank_mask:0xf\n\t"       \
+      "v_fmac_f32_dpp %2, %2, %8 quad_perm:" PERM " row_mask:0xf bank_mask:0xf\n\t"       \
+      "v_fmac_f32_dpp %3, %3, %8 quad_perm:" PERM " row_mask:0xf bank_mask:0xf\n\t"       \
+      "v_fmac_f32_dpp %4, %4, %8 quad_perm:" PERM " row_mask:0xf bank_mask:0xf\n\t"       \
+      "v_fmac_f32_dpp %5, %5, %8 quad_perm:" PERM " row_mask:0xf bank_mask:0xf\n\t"       \
+      "v_fmac_f32_dpp %6, %6, %8 quad_perm:" PERM " row_mask:0xf bank_mask:0xf\n\t"       \
+      "v_fmac_f32_dpp %7, %7, %8 quad_perm:" PERM " row_mask:0xf bank_mask:0xf"           \
+      : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]), "+v"(c[6]), \
+        "+v"(c[7])                                                                        \
+      : "v"(sgn))
+
+__device__ __forceinline__ void fmac_dpp_xor1(float (&c)[8], float sgn) {
+  DSCQ_FMAC_DPP8("[1,0,3,2]");
+}
+__device__ __forceinline__ void fmac_dpp_xor2(float (&c)[8], float sgn) {
+  DSCQ_FMAC_DPP8("[2,3,0,1]");
+}
+#undef DSCQ_FMAC_DPP8
+
+// Index bits 3..6 of one block as c[4][8] in quad lane r; afterwards the lane
+// holds sign(r) * y with sign(r) = -1 for r = 1, 2 and +1 for r = 0, 3.
+__device__ __forceinline__ void fwht_block_tail_signed(float c[4][8], int r) {
+  const float s1 = (r & 1) ? -1.0f : 1.0f;
+  const float s2 = (r & 2) ? -1.0f : 1.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) fmac_dpp_xor1(*reinterpret_cast<float(*)[8]>(c[j]), s1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) fmac_dpp_xor2(*reinterpret_cast<float(*)[8]>(c[j]), s2);
+#pragma unroll
+  for (int h = 1; h < 4; h <<= 1)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (!(j & h)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float u = c[j][i], w = c[j + h][i];
+          c[j][i] = u + w;
+          c[j + h][i] = u - w;
+        }
+      }
+}
+
+// Activation chunk -> bytes u = q, clip == 1 form: no clamp.  With clip 1 the
+// exact t lies in [-0.5, 15.5] (t = 15 - u + rne(u) at the row maximum and
+// -u + rne(u) at the minimum, u = -lo / scale), so a code outside [0, 15]
+// needs t within rounding distance of -0.5 or 15.5 -- exactly the near-tie
+// case the dmax check sends to the exact path.  cvt_pk_u8 saturates -0 to 0.
+__device__ __forceinline__ void act_chunk_fast_noclamp(const float v[8], const RowScale& rs,
+                                                       uint32_t& ev, uint32_t& od,
+                                                       float& dmax) {
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float t = __builtin_fmaf(v[i], rs.y, rs.zf);
+    q[i] = __builtin_rintf(t);
+    dmax = fmaxf(dmax, fabsf(t - q[i]));
+  }
+  ev = put_u8<0>(q[0], 0u); ev = put_u8<1>(q[2], ev); ev = put_u8<2>(q[4], ev); ev = put_u8<3>(q[6], ev);
+  od = put_u8<0>(q[1], 0u); od = put_u8<1>(q[3], od); od = put_u8<2>(q[5], od); od = put_u8<3>(q[7], od);
+}
+
 template <int MODE>
 __device__ __forceinline__ void write_row_meta(const RowArgs& a, int64_t row, bool real,
                                                const RowScale& rs, int sum) {
@@ -299,9 +401,9 @@ __device__ __forceinline__ void write_row_meta(const RowArgs& a, int64_t row, bo
   }
 }
 
-// --------------------------------------------------------- register kernel
-
-template <typename T, bool ROT, int MODE, int WPR, int ITERS>
+// FULL: every chunk of every quad lies inside K (K == nblk * 128 and
+// nblk == 16 * WPR * ITERS), so no per-chunk masking is needed.
+template <typename T, bool ROT, int MODE, int WPR, int ITERS, bool FULL>
 __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
   constexpr int ROWS = (kThreads / 64) / WPR;
   constexpr int NQ = 16 * WPR;
@@ -318,32 +420,60 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
 
   // Rows of this kernel are 16-byte aligned with K % 8 == 0 (see row_quant).
   Raw<T> raw[ITERS][4];
-  bool ok[ITERS][4];
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     const int b = quad + it * NQ;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
-      ok[it][j] = real && b < a.nblk && e0 < a.K;
-      raw[it][j] = load_raw<T>(xrow, e0, ok[it][j]);
+      const bool ok = FULL || (b < a.nblk && e0 < a.K);
+      raw[it][j] = load_raw<T>(xrow, e0, ok);
     }
   }
-  float v[ITERS][4][8];
+  // Zero what was loaded from a placeholder address: padded rows (uniform per
+  // wave) and, unless FULL, chunks past the end of the row.
+  const bool zero_row = !real;
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it)
+  for (int it = 0; it < ITERS; ++it) {
+    const int b = quad + it * NQ;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      to_f32(raw[it][j], v[it][j]);
-      mask_f32<T>(ok[it][j], v[it][j]);
+      const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
+      const bool ok = !zero_row && (FULL || (b < a.nblk && e0 < a.K));
+      if (!FULL || zero_row) {
+        uint32_t* w = reinterpret_cast<uint32_t*>(&raw[it][j]);
+#pragma unroll
+        for (int k = 0; k < (int)(sizeof(Raw<T>) / 4); ++k) w[k] = ok ? w[k] : 0u;
+      }
     }
+  }
 
+  float v[ITERS][4][8];
+  if (ROT && sizeof(T) == 2) {
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(&raw[it][j]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bfly_f16x2(w[k], v[it][j][2 * k], v[it][j][2 * k + 1]);
+        fwht_chunk_tail(v[it][j]);
+      }
+  } else {
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        to_f32(raw[it][j], v[it][j]);
+        if (ROT) fwht_chunk(v[it][j]);
+      }
+  }
+  // Lane sign after the signed transform (values held are lsign * y).
+  const float lsign = (ROT && (r == 1 || r == 2)) ? -1.0f : 1.0f;
   if (ROT) {
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) fwht_chunk(v[it][j]);
-      fwht_block_tail(v[it], r);
+      fwht_block_tail_signed(v[it], r);
       if (MODE == kWgt) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -367,6 +497,12 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
           mx = fmaxf(mx, fabsf(v[it][j][i]));
         }
       }
+  if (MODE == kAct && ROT) {
+    // Undo the lane sign: min / max of -y are -max / -min of y.
+    const float mn_l = mn, mx_l = mx;
+    mn = lsign > 0.0f ? mn_l : -mx_l;
+    mx = lsign > 0.0f ? mx_l : -mn_l;
+  }
   if (MODE == kAct) mn = wave_min(mn);
   mx = wave_max(mx);
   if (WPR > 1) {
@@ -385,22 +521,47 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
     }
   }
   const RowScale rs = row_scale<MODE>(mn, mx, a.clip, a.qmax);
+  // Lanes holding -y: the fast path folds the sign into the reciprocal
+  // ((-y) * (-1/s) == y * (1/s) exactly); the exact path and the weight path
+  // negate the values back first.
+  RowScale rs_l = rs;
+  rs_l.y = lsign * rs.y;
+  auto unsign = [&]() {
+    if (ROT && lsign < 0.0f) {
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[it][j][i] = -v[it][j][i];
+    }
+  };
 
   uint32_t ev[ITERS][4], od[ITERS][4];
   int sum = 0;
   if (MODE == kAct) {
     float dmax = 0.0f;
+    if (a.clip == 1.0f && a.qmax == 15.0f) {
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it)
+      for (int it = 0; it < ITERS; ++it)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) act_chunk_fast(v[it][j], rs, ev[it][j], od[it][j], dmax);
+        for (int j = 0; j < 4; ++j)
+          act_chunk_fast_noclamp(v[it][j], rs_l, ev[it][j], od[it][j], dmax);
+    } else {
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) act_chunk_fast(v[it][j], rs_l, ev[it][j], od[it][j], dmax);
+    }
     if (dmax > rs.thr) {
+      unsign();
 #pragma unroll
       for (int it = 0; it < ITERS; ++it)
 #pragma unroll
         for (int j = 0; j < 4; ++j) act_chunk_exact(v[it][j], rs, ev[it][j], od[it][j]);
     }
   } else {
+    unsign();
 #pragma unroll
     for (int it = 0; it < ITERS; ++it)
 #pragma unroll
@@ -423,7 +584,7 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     const int b = quad + it * NQ;
-    if (b < a.nblk) {
+    if (FULL || b < a.nblk) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         store_chunk<MODE>(a, row, (int64_t)b * 128 + j * 32 + r * 8, ev[it][j], od[it][j]);
@@ -615,11 +776,17 @@ int launch_rows_typed(const RowArgs& a, int wpr, int iters, hipStream_t stream) 
   }
   const int rows_per_wg = (kThreads / 64) / wpr;
   const dim3 grid((unsigned)((a.MP + rows_per_wg - 1) / rows_per_wg));
-#define DSCQ_ROWS(W, I)                                                                \
-  if (wpr == W && iters == I) {                                                        \
-    hipLaunchKernelGGL((row_quant_kernel<T, ROT, MODE, W, I>), grid, dim3(kThreads), 0, \
-                       stream, a);                                                     \
-    return launch_status("row_quant_kernel");                                         \
+  // Full rows: K fills exactly the 16 * wpr * iters blocks every quad walks.
+  const bool full = a.K == (int64_t)a.nblk * 128 && a.nblk == 16 * wpr * iters;
+#define DSCQ_ROWS(W, I)                                                                   \
+  if (wpr == W && iters == I) {                                                           \
+    if (full && MODE == kAct)                                                             \
+      hipLaunchKernelGGL((row_quant_kernel<T, ROT, MODE, W, I, true>), grid, dim3(kThreads), \
+                         0, stream, a);                                                   \
+    else                                                                                  \
+      hipLaunchKernelGGL((row_quant_kernel<T, ROT, MODE, W, I, false>), grid,              \
+                         dim3(kThreads), 0, stream, a);                                   \
+    return launch_status("row_quant_kernel");                                            \
   }
   DSCQ_ROWS(1, 1) DSCQ_ROWS(1, 2) DSCQ_ROWS(1, 4)
   DSCQ_ROWS(2, 1) DSCQ_ROWS(2, 2) DSCQ_ROWS(2, 4)
@@ -628,33 +795,22 @@ int launch_rows_typed(const RowArgs& a, int wpr, int iters, hipStream_t stream) 
   return fail("internal: no row kernel for wpr=%d iters=%d", wpr, iters);
 }
 
-// Register-kernel shape for a row of nblk 128-blocks: waves per row and
-// blocks per quad.  Many rows: one wave per row (no barriers); few rows:
-// spread each row over more waves.  wpr = 0 selects the streaming kernel.
+// Register-kernel shape for a row of nblk 128-blocks: waves per row (wpr)
+// and blocks per quad (iters).  Few blocks per lane keeps each wave's
+// arithmetic short, so waves whose rows arrive late finish soon after; one
+// block per quad (32 elements per lane) is preferred, spreading the row over
+// up to four waves.  wpr = 0 selects the streaming kernel.
 void pick_shape(int64_t MP, int nblk, int* wpr, int* iters) {
-  static const int kCand[9][2] = {{1, 1}, {1, 2}, {2, 1}, {1, 4}, {2, 2},
-                                  {4, 1}, {2, 4}, {4, 2}, {4, 4}};
-  const bool many_rows = MP >= 1024;
-  int best = -1;
-  for (int c = 0; c < 9; ++c) {
-    if (16 * kCand[c][0] * kCand[c][1] < nblk) continue;
-    if (best < 0) {
-      best = c;
-      continue;
-    }
-    const int w = kCand[c][0], i = kCand[c][1];
-    const int bw = kCand[best][0], bi = kCand[best][1];
-    const bool better = many_rows ? (w < bw || (w == bw && i < bi))
-                                  : (i < bi || (i == bi && w < bw));
-    if (better) best = c;
-  }
-  if (best < 0) {
-    *wpr = 0;
-    *iters = 0;
-  } else {
-    *wpr = kCand[best][0];
-    *iters = kCand[best][1];
-  }
+  (void)MP;
+  for (int i : {1, 2, 4})
+    for (int w : {1, 2, 4})
+      if (16 * w * i >= nblk) {
+        *wpr = w;
+        *iters = i;
+        return;
+      }
+  *wpr = 0;
+  *iters = 0;
 }
 
 }  // namespace
@@ -683,6 +839,17 @@ int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float 
           ((K * esize) % 16 == 0);
   int wpr, iters;
   pick_shape(MP, a.nblk, &wpr, &iters);
+  // DSCQ_QUANT_SHAPE=<wpr>x<iters> pins the register-kernel shape (tuning
+  // sweeps only); it is ignored when it cannot hold the row.
+  static const char* env = getenv("DSCQ_QUANT_SHAPE");
+  if (env) {
+    int w = 0, i = 0;
+    if (sscanf(env, "%dx%d", &w, &i) == 2 && (w == 1 || w == 2 || w == 4) &&
+        (i == 1 || i == 2 || i == 4) && 16 * w * i >= a.nblk) {
+      wpr = w;
+      iters = i;
+    }
+  }
   if (!a.vec) wpr = iters = 0;  // element-wise loads: streaming kernel only
   const bool rot = rotate_block != 0;
 #define DSCQ_T(T)                                                                    \

@@ -60,6 +60,13 @@ def parse():
                    help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-graph", action="store_true")
+    p.add_argument("--kernels-only", action="store_true",
+                   help="launch only the quantize kernel, the GEMM and a 16 MiB device copy "
+                        "(--kernel-iters each), for rocprofv3 --pmc passes")
+    p.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                   help="turn two rocprofv3 --pmc counter_collection.csv files of a "
+                        "--kernels-only run (FETCH_SIZE, WRITE_SIZE) into HBM bytes per launch, "
+                        "calibrated on the copy kernel; prints the JSON block kept under profiles/")
     return p.parse_args()
 
 
@@ -85,6 +92,57 @@ def time_kernel(launch, n, torch):
     end.record()
     end.synchronize()
     return start.elapsed_time(end) / n * 1e-3  # seconds
+
+
+COPY_BYTES = 16 << 20
+
+
+def kernel_class(name):
+    if "row_quant" in name:
+        return "quantize"
+    if "w4a4_gemm" in name:
+        return "gemm"
+    if "copy" in name.lower():
+        return "copy"
+    return None
+
+
+def traffic_summary(fetch_csv, write_csv):
+    """Mean FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel class, scaled by the
+    ratio of bytes a 16 MiB device copy really moves to what the counter reports for it."""
+    import csv
+    means = {}
+    for path, counter in ((fetch_csv, "FETCH_SIZE"), (write_csv, "WRITE_SIZE")):
+        acc = {}
+        for row in csv.DictReader(open(path)):
+            cls = kernel_class(row["Kernel_Name"])
+            if cls is None or row["Counter_Name"] != counter:
+                continue
+            acc.setdefault(cls, []).append(float(row["Counter_Value"]) * 1024.0)
+        for cls, v in acc.items():
+            means.setdefault(cls, {})[counter] = sum(v) / len(v)
+    f_fetch = COPY_BYTES / means["copy"]["FETCH_SIZE"]
+    f_write = COPY_BYTES / means["copy"]["WRITE_SIZE"]
+    out = {"calibration": {"copy_bytes_each_way": COPY_BYTES,
+                           "fetch_counter_bytes": round(means["copy"]["FETCH_SIZE"]),
+                           "write_counter_bytes": round(means["copy"]["WRITE_SIZE"]),
+                           "fetch_factor": round(f_fetch, 4), "write_factor": round(f_write, 4)}}
+    for cls in ("quantize", "gemm"):
+        if cls in means:
+            fb = means[cls]["FETCH_SIZE"] * f_fetch
+            wb = means[cls]["WRITE_SIZE"] * f_write
+            out[cls] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "traffic": round(fb + wb)}
+    return out
+
+
+def load_traffic(workload):
+    """The traffic block committed for this workload, or None."""
+    import re
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"```json\n(.*?)\n```", open(path).read(), re.S)
+    return json.loads(m.group(1)) if m else None
 
 
 def cpu_baseline(M, N, K, budget_s):
@@ -115,6 +173,9 @@ def cpu_baseline(M, N, K, budget_s):
 
 def main():
     args = parse()
+    if args.traffic:
+        print(json.dumps(traffic_summary(*args.traffic), indent=1))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(this build runs the path on a single MI355X)", file=sys.stderr)
@@ -158,6 +219,20 @@ def main():
     def step(i):
         quantize(xs[i % nbuf])
         gemm()
+
+    if args.kernels_only:
+        src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device=dev)
+        dst = torch.empty_like(src)
+        for i in range(args.kernel_iters):
+            quantize(xs[i % nbuf])
+        for i in range(args.kernel_iters):
+            gemm()
+        for i in range(args.kernel_iters):
+            dst.copy_(xs[i % nbuf].view(-1)[:src.numel()])
+        torch.cuda.synchronize()
+        print(f"kernels-only: {args.kernel_iters} launches each of quantize, gemm, "
+              f"{COPY_BYTES >> 20} MiB copy", flush=True)
+        return
 
     # ---- per-kernel device times (HIP events on the launch stream)
     qi = [0]
@@ -210,6 +285,7 @@ def main():
     qbytes = 2 * M * K + M * K // 2 + 8 * M  # read x fp16, write int4 + scale + zero
     quant_gbs = qbytes / t_quant / 1e9
 
+    traffic = load_traffic(args.workload)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(M, N, K, args.cpu_seconds)
@@ -233,13 +309,17 @@ def main():
                    "input_buffers": nbuf, "graphs": graphs is not None},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2),
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": None,
-                     "kernel": "w4a4_gemm_kernel", "avg_us": round(t_gemm * 1e6, 3),
-                     "ops_per_launch": ops},
+                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+                     "traffic": traffic["gemm"]["traffic"] if traffic and "gemm" in traffic else None,
+                     "kernel": "w4a4_gemm_pipe_kernel", "avg_us": round(t_gemm * 1e6, 3),
+                     "ops_per_launch": ops,
+                     "algorithmic_bytes": M * K // 2 + N * K // 2 + 2 * M * N},
         "kernels": {
             "quantize": {"bound": "hbm", "achieved": round(quant_gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(quant_gbs / PEAK_HBM_GBS, 4),
-                         "avg_us": round(t_quant * 1e6, 3), "bytes_per_launch": qbytes},
+                         "avg_us": round(t_quant * 1e6, 3), "bytes_per_launch": qbytes,
+                         "traffic": (traffic["quantize"]["traffic"]
+                                     if traffic and "quantize" in traffic else None)},
             "gemm": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TOPS", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "avg_us": round(t_gemm * 1e6, 3)},

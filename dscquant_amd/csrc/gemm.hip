@@ -271,22 +271,28 @@ __global__ __launch_bounds__(64 * WM * WN) void w4a4_gemm_kernel(GemmArgs g) {
 
 // ------------------------------------------------------ pipelined kernel
 // BM x BN output tile, WM x WN waves, each wave a (BM/WM) x (BN/WN) block of
-// 32 x 32 MFMA tiles.  LDS holds a K slice (64 bytes = 128 nibbles per row)
-// row-major, A rows then B rows, with the four 16-byte units of a row
-// XOR-swizzled by bits 2-3 of the row so that the 16-byte fragment reads of
-// 16 consecutive lanes (16 consecutive rows) hit distinct banks.  Lane l of a
-// fragment reads row l % 32, unit 2q + l / 32 (q = 0, 1): the low 8 bytes
-// feed MFMA step 2q, the high 8 bytes step 2q + 1 -- the same assignment for
-// A and B, so every product pairs equal k.
+// 32 x 32 MFMA tiles.  K advances in slices of 256 nibbles: 128 bytes of every
+// A and B row of the tile, staged in LDS row-major (A rows, then B rows) as
+// eight 16-byte units per row, unit u of row r stored at position
+// u ^ ((r >> 1) & 7).  With that swizzle the 16-byte accesses of any 16
+// consecutive lanes -- 16 rows x one unit on reads, 2 rows x 8 units on
+// writes -- cover all 64 banks once.  Lane l of a fragment read takes row
+// l % 32, unit 2q + l / 32 (q = 0..3): the low 8 bytes feed MFMA k-step 2q,
+// the high 8 bytes k-step 2q + 1 -- the same assignment for A and B, so every
+// product pairs equal k.
 //
-// Pipeline (one barrier per slice): global loads run two slices ahead into
-// registers; slice s + 1 is written to the idle LDS buffer while slice s
-// (already in registers) feeds the matrix cores; after the barrier the next
-// slice's fragments are read back while the last MFMA step of slice s runs.
+// Pipeline, one barrier per slice (two slices in flight in LDS):
+//   step 0        MFMAs of k-step 0; global loads of slice s + 2 issued
+//   step 1        second half of slice s's fragments read from LDS
+//   step 2        slice s + 1 (in registers since slice s - 1) written to LDS
+//   step 5        barrier, then the first half of slice s + 1's fragments read
+// The barrier also orders every read of a buffer (slice s - 1's, at or
+// before step 1 of slice s - 1) before the next write into it (step 2 of
+// slice s).
 // Each step interleaves its MFMAs with the nibble unpack of the next step's
 // fragments.  The tile's row scales / zero-points are staged in LDS once.
-// The epilogue writes each wave's fp16 (or fp32) tile to LDS and stores it
-// row-contiguously in 16-byte pieces (N % 8 == 0, 16-byte aligned output).
+// The epilogue stores runs of 4 columns per lane straight from the
+// accumulators (N % 8 == 0; out, sw, sums, bias, raw 16-byte aligned).
 
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -297,15 +303,14 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   constexpr int THREADS = 64 * WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32, NF = FM + FN;
   constexpr int ROWS = BM + BN;
-  constexpr int STAGE = ROWS * 64;
-  constexpr int LOADS = ROWS * 4 / THREADS;  // 16-byte pieces per thread per slice
-  static_assert(ROWS * 4 % THREADS == 0 && THREADS / 4 % 16 == 0, "load split");
-  constexpr int ROWB = TN * (int)sizeof(OutT) + 16;  // staged output row, padded
-  constexpr int OUT_LDS = WM * WN * TM * ROWB;
-  constexpr int MAIN_LDS = 2 * STAGE > OUT_LDS ? 2 * STAGE : OUT_LDS;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[MAIN_LDS + BM * 8];
-  float* const lds_sx = reinterpret_cast<float*>(smem + MAIN_LDS);
-  int32_t* const lds_z = reinterpret_cast<int32_t*>(smem + MAIN_LDS + BM * 4);
+  constexpr int SB = 128;         // bytes of a row per slice
+  constexpr int UNITS = SB / 16;  // 16-byte units per row per slice
+  constexpr int STAGE = ROWS * SB;
+  constexpr int LOADS = ROWS * UNITS / THREADS;  // 16-byte pieces per thread per slice
+  static_assert(ROWS * UNITS % THREADS == 0 && THREADS / UNITS % 16 == 0, "load split");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE + BM * 8];
+  float* const lds_sx = reinterpret_cast<float*>(smem + 2 * STAGE);
+  int32_t* const lds_z = reinterpret_cast<int32_t*>(smem + 2 * STAGE + BM * 4);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -316,15 +321,15 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   const int64_t m0 = (int64_t)tile_m * BM;
   const int64_t n0 = (int64_t)tile_n * BN;
   const int64_t KB = g.KP / 2;
-  const int nslices = (int)((KB + 63) / 64);
+  const int nslices = (int)((KB + SB - 1) / SB);
 
-  // Global pieces of this thread: logical unit u = tid % 4 of rows
-  // tid / 4 + (THREADS / 4) i.  Rows past MP / NP are clamped (never stored).
-  const int u = tid & 3;
+  // Global pieces of this thread: unit u = tid % UNITS of rows
+  // tid / UNITS + (THREADS / UNITS) i.  Rows past MP / NP are clamped (never stored).
+  const int u = tid % UNITS;
   const uint8_t* src[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
-    const int R = (tid >> 2) + (THREADS / 4) * i;
+    const int R = tid / UNITS + (THREADS / UNITS) * i;
     if (R < BM) {
       const int64_t row = min(m0 + R, g.arows - 1);
       src[i] = g.a + row * KB + u * 16;
@@ -333,39 +338,43 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
       src[i] = g.b + row * KB + u * 16;
     }
   }
-  // (R >> 2) & 3 == (tid >> 4) & 3 because THREADS / 4 is a multiple of 16.
-  const int wr_off = (tid >> 2) * 64 + 16 * (u ^ ((tid >> 4) & 3));
+  // (R >> 1) & 7 depends on tid only: THREADS / UNITS is a multiple of 16.
+  const int wr_off = (tid / UNITS) * SB + 16 * (u ^ ((tid / UNITS >> 1) & 7));
 
   auto gload = [&](uint4 (&st)[LOADS], int slice) {
     const int sl = min(slice, nslices - 1);
-    const int64_t kb = (int64_t)sl * 64;
+    int64_t kb = (int64_t)sl * SB;
+    // Pieces past the row end (only in the last slice when KB % SB != 0) read
+    // the row's last in-bounds piece and are zeroed.
+    const bool tail = KTAIL && kb + u * 16 >= KB;
+    if (KTAIL && tail) kb = KB - 16 - u * 16;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       uint4 v = *reinterpret_cast<const uint4*>(src[i] + kb);
-      if (KTAIL && kb + u * 16 >= KB) v = make_uint4(0u, 0u, 0u, 0u);
+      if (KTAIL && tail) v = make_uint4(0u, 0u, 0u, 0u);
       st[i] = v;
     }
   };
   auto lstore = [&](const uint4 (&st)[LOADS], int buf) {
 #pragma unroll
     for (int i = 0; i < LOADS; ++i)
-      *reinterpret_cast<uint4*>(smem + buf * STAGE + wr_off + i * (THREADS / 4) * 64) = st[i];
+      *reinterpret_cast<uint4*>(smem + buf * STAGE + wr_off + i * (THREADS / UNITS) * SB) = st[i];
   };
 
-  // Fragment read offsets (bytes within a stage) for q = 0, 1.
+  // Fragment read offsets (bytes within a stage) for q = 0..3.
   const int fr_row = lane & 31;
-  const int fr_sw = (lane >> 2) & 3;
-  int rd_off[NF][2];
+  const int fr_sw = (fr_row >> 1) & 7;
+  int rd_off[NF][4];
 #pragma unroll
   for (int f = 0; f < NF; ++f) {
     const int R = f < FM ? (wm * TM + f * 32 + fr_row) : (BM + wn * TN + (f - FM) * 32 + fr_row);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) rd_off[f][q] = R * 64 + 16 * ((2 * q + (lane >> 5)) ^ fr_sw);
+    for (int q = 0; q < 4; ++q) rd_off[f][q] = R * SB + 16 * ((2 * q + (lane >> 5)) ^ fr_sw);
   }
-  uint4 P[2][NF];
-  auto lread = [&](int buf) {
+  uint4 P[4][NF];
+  auto lread = [&](int buf, int half) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int q = 2 * half; q < 2 * half + 2; ++q)
 #pragma unroll
       for (int f = 0; f < NF; ++f)
         P[q][f] = *reinterpret_cast<const uint4*>(smem + buf * STAGE + rd_off[f][q]);
@@ -378,7 +387,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     for (int j = 0; j < FN; ++j) acc[i][j] = v16i{0};
 
   v4i U0[NF], U1[NF];
-  // step t of a slice uses P[t / 2] dwords (2 * (t % 2), +1).
+  // k-step t of a slice uses P[t / 2] dwords (2 * (t % 2), +1).
   auto unpack_step = [&](v4i (&U)[NF], int t) {
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
@@ -386,12 +395,13 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
       U[f] = (t & 1) ? unpack8(w.z, w.w) : unpack8(w.x, w.y);
     }
   };
+  // B first: acc[i][j] accumulates the transposed tile (see the epilogue).
   auto mfma_step = [&](const v4i (&U)[NF]) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(U[i], U[FM + j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(U[FM + j], U[i], acc[i][j], 0, 0, 0);
   };
   // Pins the instruction mix of one step: MFMA, a share of the VALU work,
   // MFMA, ...; the closing sched_barrier keeps every step's memory
@@ -418,26 +428,42 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   }
   lstore(G0, 0);
   lds_barrier();
-  lread(0);
+  lread(0, 0);
   unpack_step(U0, 0);
 
   // st_next holds slice s + 1 (loaded during slice s - 1); st_free held
   // slice s, already in LDS, and now receives slice s + 2.
   auto slice = [&](int s, uint4 (&st_next)[LOADS], uint4 (&st_free)[LOADS]) {
-    const int nbuf = (s + 1) & 1;
+    const int cbuf = s & 1, nbuf = cbuf ^ 1;
     mfma_step(U0);
     unpack_step(U1, 1);
     gload(st_free, s + 2);
     interleave();
     mfma_step(U1);
     unpack_step(U0, 2);
+    lread(cbuf, 1);
     interleave();
     mfma_step(U0);
     unpack_step(U1, 3);
     lstore(st_next, nbuf);
     interleave();
+    mfma_step(U1);
+    unpack_step(U0, 4);
+    interleave();
+    mfma_step(U0);
+    unpack_step(U1, 5);
+    interleave();
+    // Slice s + 1 is complete in LDS once every wave passes here; the first
+    // half of its fragments (P[0], P[1]: free since step 2) then has three
+    // steps of MFMAs to arrive.
     lds_barrier();
-    lread(nbuf);
+    lread(nbuf, 0);
+    mfma_step(U1);
+    unpack_step(U0, 6);
+    interleave();
+    mfma_step(U0);
+    unpack_step(U1, 7);
+    interleave();
     mfma_step(U1);
     unpack_step(U0, 0);
     interleave();
@@ -450,71 +476,84 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   }
   if (s < nslices) slice(s, G1, G0);
 
-  // ---- epilogue.  D[i][j] of a 32x32 tile sits in lane (j % 32) + 32 * ((i / 4) % 2),
-  // register (i % 4) + 4 * (i / 8).  Operation order of kernel/w4a4.cu:74-77;
-  // |8 - zx| <= 8 and |sums| < 2^23, so the 24-bit multiply is exact.
+  // ---- epilogue.  The MFMAs took B as their first operand, so acc[i][j] is
+  // the transposed 32 x 32 tile: output row m, column n sits in lane
+  // (m % 32) + 32 * ((n / 4) % 2), register (n % 4) + 4 * (n / 8).  Every lane
+  // therefore holds runs of 4 consecutive columns of one row and writes them
+  // straight to memory (8 bytes fp16 / 16 bytes fp32).  Operation order of
+  // kernel/w4a4.cu:74-77; |8 - zx| <= 8 and |sums| < 2^23, so the 24-bit
+  // multiply is exact.
   const OutT* bias = static_cast<const OutT*>(g.bias);
-  float swc[FN], bc[FN];
-  int32_t sumc[FN];
+  const int rl = lane & 31;
+  const int cq = 4 * (lane >> 5);
+  float sxr[FM];
+  int32_t zr[FM];
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int64_t col = n0 + wn * TN + j * 32 + (lane & 31);
-    const int64_t colc = col < g.N ? col : 0;
-    swc[j] = g.sw[colc];
-    sumc[j] = g.sums[colc];
-    bc[j] = BIAS ? (float)bias[colc] : 0.0f;
+  for (int i = 0; i < FM; ++i) {  // staged before the first barrier of the K loop
+    sxr[i] = lds_sx[wm * TM + i * 32 + rl];
+    zr[i] = lds_z[wm * TM + i * 32 + rl];
   }
-  lds_barrier();  // every wave is done with the K slices; row metadata visible
-  auto value = [&](int i, int j, int v) {
-    const int r = wm * TM + i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
-    const int32_t corrected = (acc[i][j][v] >> 8) + __mul24(lds_z[r], sumc[j]);
-    float res = (float)corrected * lds_sx[r];
-    res = res * swc[j];
-    if (BIAS) res = res + bc[j];
-    return res;
-  };
-  if (g.raw) {
-    // Raw-accumulator mode (the reference's unfused matmul): plain stores.
-    OutT* out = static_cast<OutT*>(g.out);
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t row = m0 + wm * TM + i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
-          const int64_t col = n0 + wn * TN + j * 32 + (lane & 31);
-          if (row < g.M && col < g.N) {
-            g.raw[row * g.N + col] = acc[i][j][v] >> 8;
-            out[row * g.N + col] = to_out<OutT>(value(i, j, v));
-          }
-        }
-    return;
-  }
-  // Stage the wave's TM x TN tile in LDS, then write it out row-contiguously.
-  uint8_t* tile = smem + wave * TM * ROWB;
+  float4 swc[FN][4], bc[FN][4];
+  int4 sumc[FN][4];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = i * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
-        const int c = j * 32 + (lane & 31);
-        *reinterpret_cast<OutT*>(tile + r * ROWB + c * (int)sizeof(OutT)) =
-            to_out<OutT>(value(i, j, v));
+    for (int q = 0; q < 4; ++q) {
+      const int64_t c0 = n0 + wn * TN + j * 32 + 8 * q + cq;
+      const int64_t cc = c0 < g.N ? c0 : 0;  // N % 8 == 0: c0 < N covers c0 + 3
+      swc[j][q] = *reinterpret_cast<const float4*>(g.sw + cc);
+      sumc[j][q] = *reinterpret_cast<const int4*>(g.sums + cc);
+      if (BIAS) {
+        if (sizeof(OutT) == 2) {
+          const uint2 h = *reinterpret_cast<const uint2*>(bias + cc);
+          const float2 lo = __half22float2(*reinterpret_cast<const __half2*>(&h.x));
+          const float2 hi = __half22float2(*reinterpret_cast<const __half2*>(&h.y));
+          bc[j][q] = make_float4(lo.x, lo.y, hi.x, hi.y);
+        } else {
+          bc[j][q] = *reinterpret_cast<const float4*>(bias + cc);
+        }
       }
-  constexpr int CHUNKS = TN * (int)sizeof(OutT) / 16;  // 16-byte pieces per row
-  constexpr int RPI = 64 / CHUNKS;                      // rows per wave instruction
+    }
+  auto value = [&](int i, int j, int v, float sw, int32_t sum, float b) {
+    const int32_t corrected = (acc[i][j][v] >> 8) + __mul24(zr[i], sum);
+    float res = (float)corrected * sxr[i];
+    res = res * sw;
+    if (BIAS) res = res + b;
+    return res;
+  };
   OutT* out = static_cast<OutT*>(g.out);
-  const int cpos = lane % CHUNKS;
-  const int64_t col0 = n0 + wn * TN + cpos * (16 / (int)sizeof(OutT));
 #pragma unroll
-  for (int k = 0; k < TM / RPI; ++k) {
-    const int r = k * RPI + lane / CHUNKS;
-    const uint4 w = *reinterpret_cast<const uint4*>(tile + r * ROWB + cpos * 16);
-    const int64_t row = m0 + wm * TM + r;
-    if (row < g.M && col0 < g.N) *reinterpret_cast<uint4*>(out + row * g.N + col0) = w;
+  for (int i = 0; i < FM; ++i) {
+    const int64_t row = m0 + wm * TM + i * 32 + rl;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t c0 = n0 + wn * TN + j * 32 + 8 * q + cq;
+        const float4 sw = swc[j][q];
+        const int4 sm = sumc[j][q];
+        const float4 b = bc[j][q];
+        const float r0 = value(i, j, 4 * q + 0, sw.x, sm.x, b.x);
+        const float r1 = value(i, j, 4 * q + 1, sw.y, sm.y, b.y);
+        const float r2 = value(i, j, 4 * q + 2, sw.z, sm.z, b.z);
+        const float r3 = value(i, j, 4 * q + 3, sw.w, sm.w, b.w);
+        if (row < g.M && c0 < g.N) {
+          if (sizeof(OutT) == 2) {
+            const __half h0 = to_out<__half>(r0), h1 = to_out<__half>(r1);
+            const __half h2 = to_out<__half>(r2), h3 = to_out<__half>(r3);
+            uint2 pk;
+            pk.x = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
+            pk.y = (uint32_t)__half_as_ushort(h2) | ((uint32_t)__half_as_ushort(h3) << 16);
+            *reinterpret_cast<uint2*>(out + row * g.N + c0) = pk;
+          } else {
+            *reinterpret_cast<float4*>(out + row * g.N + c0) = make_float4(r0, r1, r2, r3);
+          }
+          if (g.raw)  // the reference's raw-accumulator mode (fused = false)
+            *reinterpret_cast<int4*>(g.raw + row * g.N + c0) =
+                make_int4(acc[i][j][4 * q] >> 8, acc[i][j][4 * q + 1] >> 8,
+                          acc[i][j][4 * q + 2] >> 8, acc[i][j][4 * q + 3] >> 8);
+        }
+      }
   }
 }
 
@@ -558,12 +597,20 @@ int launch_cfg(GemmArgs g, hipStream_t stream) {
   return launch_status("w4a4_gemm_kernel");
 }
 
+// The pipelined kernel's layout requirements: whole 8-column groups, 16-byte
+// aligned output, metadata, bias and raw rows, 64+ rows.
+bool pipe_ok(const GemmArgs& g) {
+  auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+  return g.N % 8 == 0 && g.M >= 64 && al(g.out, 16) && al(g.sw, 16) && al(g.sums, 16) &&
+         al(g.raw, 16) && al(g.bias, 16);
+}
+
 // DSCQ_GEMM_TILE=<BM>x<BN>[w8] pins the tile shape (tuning sweeps only).
 template <typename OutT>
 int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
   static const char* env = getenv("DSCQ_GEMM_TILE");
   *handled = 1;
-  if (env && g.KP <= 65536) {
+  if (env && g.KP <= 65536 && (strncmp(env, "pipe", 4) != 0 || pipe_ok(g))) {
     if (!strcmp(env, "128x256")) return launch_cfg<OutT, 128, 256, 2, 2, false>(g, stream);
     if (!strcmp(env, "128x128")) return launch_cfg<OutT, 128, 128, 2, 2, false>(g, stream);
     if (!strcmp(env, "256x128")) return launch_cfg<OutT, 256, 128, 2, 2, false>(g, stream);
@@ -575,6 +622,7 @@ int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
     if (!strcmp(env, "pipe128x256")) return launch_pipe_cfg<OutT, 128, 256, 2, 2, 1>(g, stream);
     if (!strcmp(env, "pipe128")) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
     if (!strcmp(env, "pipe256x128w8")) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
+    if (!strcmp(env, "pipe256x128")) return launch_pipe_cfg<OutT, 256, 128, 2, 2, 1>(g, stream);
   }
   *handled = 0;
   return 0;
@@ -587,8 +635,7 @@ int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
   if (handled) return rc;
   if (g.KP > 65536) return launch_cfg<OutT, 64, 64, 2, 2, true>(g, stream);
   if (decode || g.M <= 32) return launch_cfg<OutT, 32, 128, 1, 4, false>(g, stream);
-  const bool aligned16 = (reinterpret_cast<uintptr_t>(g.out) & 15) == 0;
-  if (g.N % 8 == 0 && aligned16 && g.M >= 64) return launch_pipe<OutT>(g, stream);
+  if (pipe_ok(g)) return launch_pipe<OutT>(g, stream);
   const int64_t big_tiles = ((g.M + 127) / 128) * ((g.N + 255) / 256);
   if (big_tiles >= 192) return launch_cfg<OutT, 128, 256, 2, 2, false>(g, stream);
   return launch_cfg<OutT, 128, 128, 2, 2, false>(g, stream);

@@ -39,24 +39,35 @@ __device__ __forceinline__ float readlane_f32(float v, int lane) {
                             __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-// Min / max over the 64 lanes of a wave; every lane gets the result.
+// Min / max over the 64 lanes of a wave; every lane gets the result.  Each
+// 16-lane row is reduced with v_min / v_max taking one operand through DPP
+// (one instruction per step; written out because the compiler pairs a DPP
+// move with a canonicalizing max before every fminf / fmaxf).  The leading
+// s_nop covers the two wait states gfx9 needs between a VALU write and a DPP
+// read of the same register.  Inputs are finite.
+#define DSCQ_DPP_REDUCE(OP, V)                                                         \
+  asm("s_nop 1\n\t"                                                                   \
+      "v_" OP "_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"  \
+      "s_nop 1\n\t"                                                                   \
+      "v_" OP "_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"  \
+      "s_nop 1\n\t"                                                                   \
+      "v_" OP "_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"            \
+      "s_nop 1\n\t"                                                                   \
+      "v_" OP "_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf"                  \
+      : "+v"(V))
+
 __device__ __forceinline__ float wave_min(float v) {
-  v = fminf(v, dpp_f32<kDppQuadXor1>(v));
-  v = fminf(v, dpp_f32<kDppQuadXor2>(v));
-  v = fminf(v, dpp_f32<kDppRowRor4>(v));
-  v = fminf(v, dpp_f32<kDppRowRor8>(v));
+  DSCQ_DPP_REDUCE("min", v);
   return fminf(fminf(readlane_f32(v, 0), readlane_f32(v, 16)),
                fminf(readlane_f32(v, 32), readlane_f32(v, 48)));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
-  v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
-  v = fmaxf(v, dpp_f32<kDppRowRor4>(v));
-  v = fmaxf(v, dpp_f32<kDppRowRor8>(v));
+  DSCQ_DPP_REDUCE("max", v);
   return fmaxf(fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)),
                fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
 }
+#undef DSCQ_DPP_REDUCE
 
 __device__ __forceinline__ int wave_sum_i32(int v) {
   v += __builtin_amdgcn_mov_dpp(v, kDppQuadXor1, 0xF, 0xF, false);

@@ -23,15 +23,16 @@
 //
 // Exact division at bandwidth.  The reference computes
 // code = clamp(round_half_even(fl(fl(x / s) + z))).  Per element we use
-// t = fma(x, y, z) with y = rcp(s) (relative error <= 2^-23) computed once per
-// row.  Writing Q = x / s, the exact x*y is within 2^-23 |Q| of Q and fl(Q)
-// within 2^-24 |Q|; each side is rounded once more to T-sized numbers
-// (T <= |Q| + qmax, ulp(T) <= 2^-23 T), so |t - fl(fl(Q) + z)| <=
-// 2^-23 (2.5 |Q| + qmax).  If t lies further than
-// delta = (|Q|max + qmax + 1) * 2^-21 (at least 1.6x that bound) from every
-// half-integer, t and the exact value round to the same integer; a lane that
-// sees any element closer than that recomputes all its elements with IEEE
-// division (rare: ~1e-4 of lanes).
+// t' = fma(x, y, z) with y = rcp(s) (relative error <= 2^-23) computed once
+// per row.  With Q = x / s exact, a = fl(Q) and t = fl(a + z):
+//   t  = Q + Q d1 + z + (a + z) d2,         |d1|, |d2| <= 2^-24
+//   t' = Q + Q e  + z + (Q(1 + e) + z) d3,  |e| <= 2^-23, |d3| <= 2^-24
+// so |t - t'| <= 2^-24 (5 |Q| + 2 z) up to terms of order 2^-47 |Q|.  If
+// |t' - rne(t')| < 0.5 - B with B = (5 Qmax + 2 z + 3) 2^-24 (Qmax an upper
+// bound of |Q| over the row; the +3 absorbs the roundings of B itself and of
+// 0.5 - B), t is on the same side of every half-integer as t' and both round
+// to the same integer.  A chunk of 8 elements with any element closer than
+// that is recomputed with IEEE division (a few chunks per thousand).
 // Clamping commutes with rounding because the bounds are integers.
 
 #include <cstdio>
@@ -208,12 +209,15 @@ __device__ __forceinline__ void act_chunk_fast(const float v[8], const RowScale&
 }
 
 // Activation chunk with correctly rounded division (the reference's exact rule).
+// The chunk holds sgn * x; dividing by sgn * s gives fl(x / s) exactly, since
+// IEEE division is symmetric under sign changes.
 __device__ __forceinline__ void act_chunk_exact(const float v[8], const RowScale& rs,
-                                                uint32_t& ev, uint32_t& od) {
+                                                float sgn, uint32_t& ev, uint32_t& od) {
+  const float ss = sgn * rs.scale;
   float q[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    q[i] = __builtin_amdgcn_fmed3f(__builtin_rintf(v[i] / rs.scale + rs.zf), 0.0f, rs.qmax);
+    q[i] = __builtin_amdgcn_fmed3f(__builtin_rintf(v[i] / ss + rs.zf), 0.0f, rs.qmax);
   ev = put_u8<0>(q[0], 0u); ev = put_u8<1>(q[2], ev); ev = put_u8<2>(q[4], ev); ev = put_u8<3>(q[6], ev);
   od = put_u8<0>(q[1], 0u); od = put_u8<1>(q[3], od); od = put_u8<2>(q[5], od); od = put_u8<3>(q[7], od);
 }
@@ -247,8 +251,10 @@ __device__ __forceinline__ RowScale row_scale(float mn, float mx, float clip,
     rs.zf = __builtin_amdgcn_fmed3f(__builtin_rintf(-lo / rs.scale), 0.0f, qmax);
     // Only the fast path uses y; a 1-ulp reciprocal is inside its margin.
     rs.y = __builtin_amdgcn_rcpf(rs.scale);
-    const float qbound = fmaxf(mx, -mn) / rs.scale;
-    rs.thr = 0.5f - (qbound + qmax + 1.0f) * 0x1p-21f;
+    // Upper bound of |x| / scale over the row: |x| <= max(mx, -mn), and the
+    // factor covers the reciprocal's and the product's rounding.
+    const float qbound = fmaxf(mx, -mn) * rs.y * (1.0f + 0x1p-20f);
+    rs.thr = 0.5f - (5.0f * qbound + 2.0f * rs.zf + 3.0f) * 0x1p-24f;
   } else {
     // core/quantization.py:9 (amax * clip / bound, then the 1e-8 floor).
     rs.scale = fmaxf(mx * clip / qmax, 1e-8f);
@@ -540,26 +546,18 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
   uint32_t ev[ITERS][4], od[ITERS][4];
   int sum = 0;
   if (MODE == kAct) {
-    float dmax = 0.0f;
-    if (a.clip == 1.0f && a.qmax == 15.0f) {
+    const bool noclamp = a.clip == 1.0f && a.qmax == 15.0f;
 #pragma unroll
-      for (int it = 0; it < ITERS; ++it)
+    for (int it = 0; it < ITERS; ++it)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j) {
+        float dmax = 0.0f;
+        if (noclamp)
           act_chunk_fast_noclamp(v[it][j], rs_l, ev[it][j], od[it][j], dmax);
-    } else {
-#pragma unroll
-      for (int it = 0; it < ITERS; ++it)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) act_chunk_fast(v[it][j], rs_l, ev[it][j], od[it][j], dmax);
-    }
-    if (dmax > rs.thr) {
-      unsign();
-#pragma unroll
-      for (int it = 0; it < ITERS; ++it)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) act_chunk_exact(v[it][j], rs, ev[it][j], od[it][j]);
-    }
+        else
+          act_chunk_fast(v[it][j], rs_l, ev[it][j], od[it][j], dmax);
+        if (dmax >= rs.thr) act_chunk_exact(v[it][j], rs, lsign, ev[it][j], od[it][j]);
+      }
   } else {
     unsign();
 #pragma unroll
@@ -682,12 +680,11 @@ __global__ __launch_bounds__(kThreads) void row_quant_stream_kernel(RowArgs a) {
     load_block<T, ROT, MODE>(a, xrow, real, b, r, c);
     uint32_t ev[4], od[4];
     if (MODE == kAct) {
-      float dmax = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) act_chunk_fast(c[j], rs, ev[j], od[j], dmax);
-      if (dmax > rs.thr) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) act_chunk_exact(c[j], rs, ev[j], od[j]);
+      for (int j = 0; j < 4; ++j) {
+        float dmax = 0.0f;
+        act_chunk_fast(c[j], rs, ev[j], od[j], dmax);
+        if (dmax >= rs.thr) act_chunk_exact(c[j], rs, 1.0f, ev[j], od[j]);
       }
     } else {
 #pragma unroll

@@ -281,18 +281,20 @@ __global__ __launch_bounds__(64 * WM * WN) void w4a4_gemm_kernel(GemmArgs g) {
 // the high 8 bytes k-step 2q + 1 -- the same assignment for A and B, so every
 // product pairs equal k.
 //
-// Pipeline, one barrier per slice (two slices in flight in LDS):
-//   step 0        MFMAs of k-step 0; global loads of slice s + 2 issued
-//   step 1        second half of slice s's fragments read from LDS
-//   step 2        slice s + 1 (in registers since slice s - 1) written to LDS
-//   step 5        barrier, then the first half of slice s + 1's fragments read
+// Pipeline, one barrier per slice (two slices in flight in LDS), memory
+// operations spread over the steps so LDS traffic never comes in one burst:
+//   steps 0-2     slice s + 1 (in registers since slice s - 1) written to LDS;
+//                 global loads of slice s + 2 issued at step 0
+//   steps 1, 3    fragment units q = 2, 3 of slice s read from LDS
+//   step 5        barrier; units q = 0 (step 5) and 1 (step 6) of slice s + 1
 // The barrier also orders every read of a buffer (slice s - 1's, at or
 // before step 1 of slice s - 1) before the next write into it (step 2 of
 // slice s).
 // Each step interleaves its MFMAs with the nibble unpack of the next step's
 // fragments.  The tile's row scales / zero-points are staged in LDS once.
 // The epilogue stores runs of 4 columns per lane straight from the
-// accumulators (N % 8 == 0; out, sw, sums, bias, raw 16-byte aligned).
+// accumulators (N % 8 == 0; out and raw 16-byte aligned).  Row and column
+// metadata (sx, zx, sw, sums, bias) are staged in LDS with the first slice.
 
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -308,9 +310,12 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   constexpr int STAGE = ROWS * SB;
   constexpr int LOADS = ROWS * UNITS / THREADS;  // 16-byte pieces per thread per slice
   static_assert(ROWS * UNITS % THREADS == 0 && THREADS / UNITS % 16 == 0, "load split");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE + BM * 8];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE + BM * 8 + BN * 12];
   float* const lds_sx = reinterpret_cast<float*>(smem + 2 * STAGE);
   int32_t* const lds_z = reinterpret_cast<int32_t*>(smem + 2 * STAGE + BM * 4);
+  float* const lds_sw = reinterpret_cast<float*>(smem + 2 * STAGE + BM * 8);
+  int32_t* const lds_sum = reinterpret_cast<int32_t*>(smem + 2 * STAGE + BM * 8 + BN * 4);
+  float* const lds_b = reinterpret_cast<float*>(smem + 2 * STAGE + BM * 8 + BN * 8);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -355,11 +360,16 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
       st[i] = v;
     }
   };
-  auto lstore = [&](const uint4 (&st)[LOADS], int buf) {
+  // Pieces [I0, I1) of a slice held in registers -> LDS stage `buf`.
+  auto lstore = [&](const uint4 (&st)[LOADS], int buf, auto i0, auto i1) {
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i)
+    for (int i = decltype(i0)::value; i < decltype(i1)::value; ++i)
       *reinterpret_cast<uint4*>(smem + buf * STAGE + wr_off + i * (THREADS / UNITS) * SB) = st[i];
   };
+  using C0 = std::integral_constant<int, 0>;
+  using C1 = std::integral_constant<int, (LOADS + 2) / 3>;
+  using C2 = std::integral_constant<int, (2 * LOADS + 2) / 3>;
+  using C3 = std::integral_constant<int, LOADS>;
 
   // Fragment read offsets (bytes within a stage) for q = 0..3.
   const int fr_row = lane & 31;
@@ -372,12 +382,10 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     for (int q = 0; q < 4; ++q) rd_off[f][q] = R * SB + 16 * ((2 * q + (lane >> 5)) ^ fr_sw);
   }
   uint4 P[4][NF];
-  auto lread = [&](int buf, int half) {
+  auto lread = [&](int buf, int q) {
 #pragma unroll
-    for (int q = 2 * half; q < 2 * half + 2; ++q)
-#pragma unroll
-      for (int f = 0; f < NF; ++f)
-        P[q][f] = *reinterpret_cast<const uint4*>(smem + buf * STAGE + rd_off[f][q]);
+    for (int f = 0; f < NF; ++f)
+      P[q][f] = *reinterpret_cast<const uint4*>(smem + buf * STAGE + rd_off[f][q]);
   };
 
   v16i acc[FM][FN];
@@ -419,16 +427,23 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   uint4 G0[LOADS], G1[LOADS];
   gload(G0, 0);
   gload(G1, 1);
-  // Row metadata of the tile, once per workgroup (after the slice loads, so
-  // the first slice is not queued behind it).
+  // Row and column metadata of the tile, once per workgroup (after the slice
+  // loads, so the first slice is not queued behind it).
   if (tid < BM) {
     const int64_t row = min(m0 + tid, g.arows - 1);
     lds_sx[tid] = g.sx[row];
     lds_z[tid] = 8 - g.zx[row];
   }
-  lstore(G0, 0);
+  if (tid < BN) {
+    const int64_t col = min(n0 + tid, g.brows - 1);
+    lds_sw[tid] = g.sw[col];
+    lds_sum[tid] = g.sums[col];
+    if (BIAS) lds_b[tid] = (float)static_cast<const OutT*>(g.bias)[min(n0 + tid, g.N - 1)];
+  }
+  lstore(G0, 0, C0{}, C3{});
   lds_barrier();
   lread(0, 0);
+  lread(0, 1);
   unpack_step(U0, 0);
 
   // st_next holds slice s + 1 (loaded during slice s - 1); st_free held
@@ -438,24 +453,27 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     mfma_step(U0);
     unpack_step(U1, 1);
     gload(st_free, s + 2);
+    lstore(st_next, nbuf, C0{}, C1{});
     interleave();
     mfma_step(U1);
     unpack_step(U0, 2);
-    lread(cbuf, 1);
+    lread(cbuf, 2);
+    lstore(st_next, nbuf, C1{}, C2{});
     interleave();
     mfma_step(U0);
     unpack_step(U1, 3);
-    lstore(st_next, nbuf);
+    lstore(st_next, nbuf, C2{}, C3{});
     interleave();
     mfma_step(U1);
     unpack_step(U0, 4);
+    lread(cbuf, 3);
     interleave();
     mfma_step(U0);
     unpack_step(U1, 5);
     interleave();
-    // Slice s + 1 is complete in LDS once every wave passes here; the first
-    // half of its fragments (P[0], P[1]: free since step 2) then has three
-    // steps of MFMAs to arrive.
+    // Slice s + 1 is complete in LDS once every wave passes here; its first
+    // fragments (P[0], P[1]: free since step 2) are read over the next two
+    // steps.
     lds_barrier();
     lread(nbuf, 0);
     mfma_step(U1);
@@ -463,6 +481,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     interleave();
     mfma_step(U0);
     unpack_step(U1, 7);
+    lread(nbuf, 1);
     interleave();
     mfma_step(U1);
     unpack_step(U0, 0);
@@ -483,13 +502,14 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   // straight to memory (8 bytes fp16 / 16 bytes fp32).  Operation order of
   // kernel/w4a4.cu:74-77; |8 - zx| <= 8 and |sums| < 2^23, so the 24-bit
   // multiply is exact.
-  const OutT* bias = static_cast<const OutT*>(g.bias);
+  // Row and column metadata were staged in LDS before the first barrier of
+  // the K loop.
   const int rl = lane & 31;
   const int cq = 4 * (lane >> 5);
   float sxr[FM];
   int32_t zr[FM];
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {  // staged before the first barrier of the K loop
+  for (int i = 0; i < FM; ++i) {
     sxr[i] = lds_sx[wm * TM + i * 32 + rl];
     zr[i] = lds_z[wm * TM + i * 32 + rl];
   }
@@ -499,20 +519,10 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   for (int j = 0; j < FN; ++j)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int64_t c0 = n0 + wn * TN + j * 32 + 8 * q + cq;
-      const int64_t cc = c0 < g.N ? c0 : 0;  // N % 8 == 0: c0 < N covers c0 + 3
-      swc[j][q] = *reinterpret_cast<const float4*>(g.sw + cc);
-      sumc[j][q] = *reinterpret_cast<const int4*>(g.sums + cc);
-      if (BIAS) {
-        if (sizeof(OutT) == 2) {
-          const uint2 h = *reinterpret_cast<const uint2*>(bias + cc);
-          const float2 lo = __half22float2(*reinterpret_cast<const __half2*>(&h.x));
-          const float2 hi = __half22float2(*reinterpret_cast<const __half2*>(&h.y));
-          bc[j][q] = make_float4(lo.x, lo.y, hi.x, hi.y);
-        } else {
-          bc[j][q] = *reinterpret_cast<const float4*>(bias + cc);
-        }
-      }
+      const int cl = wn * TN + j * 32 + 8 * q + cq;
+      swc[j][q] = *reinterpret_cast<const float4*>(lds_sw + cl);
+      sumc[j][q] = *reinterpret_cast<const int4*>(lds_sum + cl);
+      if (BIAS) bc[j][q] = *reinterpret_cast<const float4*>(lds_b + cl);
     }
   auto value = [&](int i, int j, int v, float sw, int32_t sum, float b) {
     const int32_t corrected = (acc[i][j][v] >> 8) + __mul24(zr[i], sum);
@@ -598,11 +608,10 @@ int launch_cfg(GemmArgs g, hipStream_t stream) {
 }
 
 // The pipelined kernel's layout requirements: whole 8-column groups, 16-byte
-// aligned output, metadata, bias and raw rows, 64+ rows.
+// aligned output and raw rows, 64+ rows.
 bool pipe_ok(const GemmArgs& g) {
   auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
-  return g.N % 8 == 0 && g.M >= 64 && al(g.out, 16) && al(g.sw, 16) && al(g.sums, 16) &&
-         al(g.raw, 16) && al(g.bias, 16);
+  return g.N % 8 == 0 && g.M >= 64 && al(g.out, 16) && al(g.raw, 16);
 }
 
 // DSCQ_GEMM_TILE=<BM>x<BN>[w8] pins the tile shape (tuning sweeps only).

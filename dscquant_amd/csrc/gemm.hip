@@ -572,7 +572,7 @@ int launch_pipe_cfg(GemmArgs g, hipStream_t stream) {
   g.tiles_n = (int)((g.N + BN - 1) / BN);
   const int64_t nblocks = ((g.M + BM - 1) / BM) * g.tiles_n;
   if (nblocks > 0x7FFFFFFF) return fail("matmul: grid too large");
-  const bool ktail = (g.KP / 2) % 64 != 0;
+  const bool ktail = (g.KP / 2) % 128 != 0;  // rows end inside a 128-byte slice
   const dim3 grid((unsigned)nblocks), block(64 * WM * WN);
 #define DSCQ_PIPE(KT, BI)                                                                  \
   hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<OutT, BM, BN, WM, WN, MINB, KT, BI>), grid, block, \

@@ -62,6 +62,10 @@ MM_CASES = [
     (512, 4096, 11008, False, False, False),
     (1000, 1000, 1024, True, True, False),
     (2048, 4096, 4096, False, False, False),
+    # packed rows ending halfway through a 256-nibble K slice (K % 256 == 128)
+    (96, 136, 128, True, False, False),
+    (200, 264, 384, False, True, False),
+    (256, 512, 4224, True, False, False),
 ]
 
 

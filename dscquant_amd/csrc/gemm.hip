@@ -607,6 +607,103 @@ int launch_cfg(GemmArgs g, hipStream_t stream) {
   return launch_status("w4a4_gemm_kernel");
 }
 
+// ------------------------------------------------------ skinny-M kernel
+// M <= 16 (decode) or force_decode: the weights are streamed once and the
+// work is split over K instead of M.  A workgroup owns 16 output columns
+// (B rows) and 16 output rows of A; its 8 waves take consecutive slices of
+// K.  Per 64-byte block of a row (128 nibbles) lane l loads 16 bytes of A
+// row l % 16 and of B row l % 16 at byte 16 * (l / 16); their low / high
+// halves feed two v_mfma_i32_16x16x64_i8 (A and B use the same k order).
+// Partial 16 x 16 sums meet in LDS; the epilogue is the reference's.
+// Bytes per launch: N * KP / 2 (weights) + the small A, read once per column
+// block from L2.
+template <typename OutT, bool BIAS>
+__global__ __launch_bounds__(512) void w4a4_gemv_kernel(GemmArgs g) {
+  constexpr int WAVES = 8;
+  __shared__ int32_t part[WAVES][16][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t n0 = (int64_t)blockIdx.x * 16, m0 = (int64_t)blockIdx.y * 16;
+  const int r = lane & 15, grp = lane >> 4;
+  const int64_t KB = g.KP / 2;
+  const int64_t nblk = (KB + 63) / 64;
+  const int64_t per = (nblk + WAVES - 1) / WAVES;
+  const int64_t b0 = wave * per, b1 = min(b0 + per, nblk);
+  const uint8_t* arow = g.a + min(m0 + r, g.arows - 1) * KB;
+  const uint8_t* brow = g.b + min(n0 + r, g.brows - 1) * KB;
+  const int64_t off = grp * 16;
+
+  v4i acc = {0, 0, 0, 0};
+  int32_t tot[4] = {0, 0, 0, 0};
+  auto piece = [&](const uint8_t* row, int64_t kb) {
+    // The last block of a row with KB % 64 == 32 is half empty: its upper
+    // pieces re-read the row's last piece and are zeroed.
+    const bool in = kb + off < KB;
+    uint4 v = *reinterpret_cast<const uint4*>(row + (in ? kb + off : KB - 16));
+    if (!in) v = make_uint4(0u, 0u, 0u, 0u);
+    return v;
+  };
+  constexpr int U = 4;  // blocks in flight per wave
+  int64_t blk = b0;
+  for (; blk + U <= b1; blk += U) {
+    uint4 av[U], bv[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      av[i] = piece(arow, (blk + i) * 64);
+      bv[i] = piece(brow, (blk + i) * 64);
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(av[i].x, av[i].y),
+                                                  unpack8(bv[i].x, bv[i].y), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(av[i].z, av[i].w),
+                                                  unpack8(bv[i].z, bv[i].w), acc, 0, 0, 0);
+    }
+    // |partial| <= 2^14 per product: drain every 65536 k (512 blocks).
+    if (((blk - b0) / U + 1) % (512 / U) == 0) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) tot[v] += acc[v] >> 8;
+      acc = v4i{0, 0, 0, 0};
+    }
+  }
+  for (; blk < b1; ++blk) {
+    const uint4 a4 = piece(arow, blk * 64), b4 = piece(brow, blk * 64);
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(a4.x, a4.y), unpack8(b4.x, b4.y), acc,
+                                                0, 0, 0);
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(a4.z, a4.w), unpack8(b4.z, b4.w), acc,
+                                                0, 0, 0);
+  }
+  // D of a 16 x 16 tile: row (A) 4 * (lane / 16) + v, column (B) lane % 16.
+#pragma unroll
+  for (int v = 0; v < 4; ++v) part[wave][4 * grp + v][r] = tot[v] + (acc[v] >> 8);
+  __syncthreads();
+  if (tid >= 256) return;
+  const int ml = tid >> 4, nl = tid & 15;
+  int32_t raw = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) raw += part[w][ml][nl];
+  const int64_t m = m0 + ml, n = n0 + nl;
+  if (m >= g.M || n >= g.N) return;
+  // Operation order of kernel/w4a4.cu:74-77.
+  const int32_t corrected = raw + (8 - g.zx[m]) * g.sums[n];
+  float res = (float)corrected * g.sx[m];
+  res = res * g.sw[n];
+  if (BIAS) res = res + (float)static_cast<const OutT*>(g.bias)[n];
+  static_cast<OutT*>(g.out)[m * g.N + n] = to_out<OutT>(res);
+  if (g.raw) g.raw[m * g.N + n] = raw;
+}
+
+template <typename OutT>
+int launch_gemv(GemmArgs g, hipStream_t stream) {
+  const int64_t gx = (g.N + 15) / 16, gy = (g.M + 15) / 16;
+  if (gx > 0x7FFFFFFF || gy > 65535) return fail("matmul: grid too large");
+  const dim3 grid((unsigned)gx, (unsigned)gy), block(512);
+  if (g.bias)
+    hipLaunchKernelGGL((w4a4_gemv_kernel<OutT, true>), grid, block, 0, stream, g);
+  else
+    hipLaunchKernelGGL((w4a4_gemv_kernel<OutT, false>), grid, block, 0, stream, g);
+  return launch_status("w4a4_gemv_kernel");
+}
+
 // The pipelined kernel's layout requirements: whole 8-column groups, 16-byte
 // aligned output and raw rows, 64+ rows.
 bool pipe_ok(const GemmArgs& g) {
@@ -628,6 +725,7 @@ int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
     if (!strcmp(env, "256x128w8")) return launch_cfg<OutT, 256, 128, 4, 2, false>(g, stream);
     if (!strcmp(env, "64x128")) return launch_cfg<OutT, 64, 128, 2, 2, false>(g, stream);
     if (!strcmp(env, "pipe")) return launch_pipe<OutT>(g, stream);
+    if (!strcmp(env, "gemv")) return launch_gemv<OutT>(g, stream);
     if (!strcmp(env, "pipe128x256")) return launch_pipe_cfg<OutT, 128, 256, 2, 2, 1>(g, stream);
     if (!strcmp(env, "pipe128")) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
     if (!strcmp(env, "pipe256x128w8")) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
@@ -642,8 +740,9 @@ int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
   int handled = 0;
   const int rc = tile_override<OutT>(g, stream, &handled);
   if (handled) return rc;
+  if (decode || g.M <= 16) return launch_gemv<OutT>(g, stream);
   if (g.KP > 65536) return launch_cfg<OutT, 64, 64, 2, 2, true>(g, stream);
-  if (decode || g.M <= 32) return launch_cfg<OutT, 32, 128, 1, 4, false>(g, stream);
+  if (g.M <= 32) return launch_cfg<OutT, 32, 128, 1, 4, false>(g, stream);
   if (pipe_ok(g)) return launch_pipe<OutT>(g, stream);
   const int64_t big_tiles = ((g.M + 127) / 128) * ((g.N + 255) / 256);
   if (big_tiles >= 192) return launch_cfg<OutT, 128, 256, 2, 2, false>(g, stream);

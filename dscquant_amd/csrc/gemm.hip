@@ -586,13 +586,14 @@ int launch_pipe_cfg(GemmArgs g, hipStream_t stream) {
   return launch_status("w4a4_gemm_pipe_kernel");
 }
 
-// 256 x 128 tiles with two waves per SIMD when they fill the chip, else
-// 128 x 128 tiles (two workgroups per CU).
+// The largest tile that still gives every CU a workgroup: 256 x 128 (two
+// waves per SIMD), else 128 x 128 or 64 x 128 (two workgroups per CU).
 template <typename OutT>
 int launch_pipe(GemmArgs g, hipStream_t stream) {
-  const int64_t big = ((g.M + 255) / 256) * ((g.N + 127) / 128);
-  if (big >= 256) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
-  return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
+  const int64_t tn = (g.N + 127) / 128;
+  if (((g.M + 255) / 256) * tn >= 256) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
+  if (((g.M + 127) / 128) * tn >= 256) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
+  return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2>(g, stream);
 }
 
 template <typename OutT, int BM, int BN, int WM, int WN, bool HUGE>
@@ -728,6 +729,7 @@ int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
     if (!strcmp(env, "gemv")) return launch_gemv<OutT>(g, stream);
     if (!strcmp(env, "pipe128x256")) return launch_pipe_cfg<OutT, 128, 256, 2, 2, 1>(g, stream);
     if (!strcmp(env, "pipe128")) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
+    if (!strcmp(env, "pipe64x128")) return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2>(g, stream);
     if (!strcmp(env, "pipe256x128w8")) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
     if (!strcmp(env, "pipe256x128")) return launch_pipe_cfg<OutT, 256, 128, 2, 2, 1>(g, stream);
   }

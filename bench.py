@@ -112,7 +112,7 @@ COPY_BYTES = 16 << 20
 def kernel_class(name):
     if "row_quant" in name:
         return "quantize"
-    if "w4a4_gemm" in name:
+    if "w4a4_gemm" in name or "w4a4_gemv" in name:
         return "gemm"
     if "copy" in name.lower():
         return "copy"
@@ -233,14 +233,16 @@ def main():
         gemm()
 
     if args.kernels_only:
-        src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device=dev)
-        dst = torch.empty_like(src)
+        # copy sources cycle through more than the 256 MiB Infinity Cache
+        srcs = [torch.ones(COPY_BYTES // 2, dtype=torch.float16, device=dev)
+                for _ in range(2 * MALL_BYTES // COPY_BYTES + 2)]
+        dst = torch.empty_like(srcs[0])
         for i in range(args.kernel_iters):
             quantize(xs[i % nbuf])
         for i in range(args.kernel_iters):
             gemm()
         for i in range(args.kernel_iters):
-            dst.copy_(xs[i % nbuf].view(-1)[:src.numel()])
+            dst.copy_(srcs[i % len(srcs)])
         torch.cuda.synchronize()
         print(f"kernels-only: {args.kernel_iters} launches each of quantize, gemm, "
               f"{COPY_BYTES >> 20} MiB copy", flush=True)

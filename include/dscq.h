@@ -113,9 +113,9 @@ int dscq_weight_codes(const void* w, int w_dtype, int64_t N, int64_t K,
  *   KP    packed width * 2; a multiple of 64, 64 <= KP <= 1048576.
  *   fused 1: out only (raw may be NULL); 0: out and raw [M, N] int32
  *         (the reference's raw-accumulator mode).
- *   force_decode  selects the skinny-M kernel (the reference's decode_gemm)
- *         regardless of M; it is also chosen for M < 8.  Results are
- *         identical either way.
+ *   force_decode  selects the skinny-M kernel (the reference's decode_gemm,
+ *         dispatched there for M < 8) regardless of M; it is also chosen for
+ *         M <= 16.  Results are identical either way.
  *   out_fp32  0: out is fp16 [M, N]; 1: fp32.
  * Limits (w4a4.cu:197): 1 <= M <= 65535, N >= 1.
  */

@@ -16,6 +16,9 @@ int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float 
               float* scales, int32_t* zeros, int32_t* sums, hipStream_t stream);
 int pack_codes(const uint8_t* codes, uint8_t* packed, int64_t MP, int64_t KP,
                hipStream_t stream);
+int silu_mul_quant(const void* gate, const void* up, int64_t ld, int64_t M, int64_t N,
+                   int64_t MP, float clip, int rotate_block, uint8_t* packed, float* scales,
+                   int32_t* zeros, void* hout, hipStream_t stream);
 int pack_int4(const int8_t* codes, int64_t R, int64_t C, uint8_t* packed,
               hipStream_t stream);
 int unpack_int4(const uint8_t* packed, int64_t R, int64_t CB, int64_t width,
@@ -99,6 +102,20 @@ int dscq_quantize(const void* x, int x_dtype, int64_t M, int64_t K, float clip, 
                          codes, scales, zeros, nullptr, s))
     return rc;
   return pack_codes(codes, packed, MP, KP, s);
+}
+
+int dscq_silu_mul_quantize(const void* gate, const void* up, int64_t ld, int64_t M,
+                           int64_t N, float clip, int rotate_block, uint8_t* packed,
+                           float* scales, int32_t* zeros, void* h, void* stream) {
+  if (!(M > 0 && M <= 65535 && N > 0 && N <= 32768))
+    return fail("silu_mul_quantize: require 1<=M<=65535 and 1<=N<=32768");
+  if (ld < N) return fail("silu_mul_quantize: row stride %lld is below N=%lld", (long long)ld,
+                          (long long)N);
+  if (!(clip >= 0.5f && clip <= 1.0f)) return fail("Activation clip must be in [0.5,1]");
+  if (int rc = check_rotation(rotate_block, N)) return rc;
+  if (!gate || !up || !packed || !scales || !zeros) return fail("silu_mul_quantize: null buffer");
+  return silu_mul_quant(gate, up, ld, M, N, ceil_to(M, 8), clip, rotate_block, packed, scales,
+                        zeros, h, static_cast<hipStream_t>(stream));
 }
 
 int dscq_activation_codes(const void* x, int x_dtype, int64_t M, int64_t K, float clip,

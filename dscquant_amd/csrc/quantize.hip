@@ -60,6 +60,9 @@ struct RowArgs {
   int32_t* zeros;      // [MP] act zero-points or null
   int32_t* sums;       // [MP] weight code sums or null
   int vec;             // rows 16-byte aligned and K % 8 == 0
+  int64_t ldx;         // elements between consecutive rows of x (and up)
+  const void* up;      // gated input: up [M, ldx] fp16, or null
+  __half* hout;        // gated input: the activation h [M, K] fp16, or null
 };
 
 // ------------------------------------------------------------------ loading
@@ -409,7 +412,23 @@ __device__ __forceinline__ void write_row_meta(const RowArgs& a, int64_t row, bo
 
 // FULL: every chunk of every quad lies inside K (K == nblk * 128 and
 // nblk == 16 * WPR * ITERS), so no per-chunk masking is needed.
-template <typename T, bool ROT, int MODE, int WPR, int ITERS, bool FULL>
+// Gated input (the SiLU-gated MLP between its up and down projections): the
+// row is h = fp16(fp16(silu(g)) * u) of two fp16 rows g (x) and u (up), the
+// roundings an fp16 model applies to act_fn(gate) and to the product.
+__device__ __forceinline__ uint32_t silu_mul_f16x2(uint32_t g2, uint32_t u2) {
+  uint32_t h2 = 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float g = h2f((g2 >> (16 * i)) & 0xFFFFu);
+    const float u = h2f((u2 >> (16 * i)) & 0xFFFFu);
+    const float sg = __half2float(__float2half_rn(g / (1.0f + __builtin_expf(-g))));
+    const __half h = __float2half_rn(sg * u);
+    h2 |= (uint32_t)__half_as_ushort(h) << (16 * i);
+  }
+  return h2;
+}
+
+template <typename T, bool ROT, int MODE, int WPR, int ITERS, bool FULL, bool GATED = false>
 __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
   constexpr int ROWS = (kThreads / 64) / WPR;
   constexpr int NQ = 16 * WPR;
@@ -422,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
   const bool real = row < a.M;
   const int quad = wave_in_row * 16 + (lane >> 2);
   const int r = lane & 3;
-  const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.K;
+  const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.ldx;
 
   // Rows of this kernel are 16-byte aligned with K % 8 == 0 (see row_quant).
   Raw<T> raw[ITERS][4];
@@ -435,6 +454,29 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
       const bool ok = FULL || (b < a.nblk && e0 < a.K);
       raw[it][j] = load_raw<T>(xrow, e0, ok);
     }
+  }
+  if (GATED) {
+    static_assert(!GATED || sizeof(T) == 2, "gated rows are fp16");
+    const T* urow = static_cast<const T*>(a.up) + (real ? row : 0) * a.ldx;
+    Raw<T> rup[ITERS][4];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int b = quad + it * NQ;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
+        rup[it][j] = load_raw<T>(urow, e0, FULL || (b < a.nblk && e0 < a.K));
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t* w = reinterpret_cast<uint32_t*>(&raw[it][j]);
+        const uint32_t* wu = reinterpret_cast<const uint32_t*>(&rup[it][j]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = silu_mul_f16x2(w[k], wu[k]);
+      }
   }
   // Zero what was loaded from a placeholder address: padded rows (uniform per
   // wave) and, unless FULL, chunks past the end of the row.
@@ -451,6 +493,8 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
 #pragma unroll
         for (int k = 0; k < (int)(sizeof(Raw<T>) / 4); ++k) w[k] = ok ? w[k] : 0u;
       }
+      if (GATED && a.hout && real && (FULL || (b < a.nblk && e0 < a.K)))
+        *reinterpret_cast<uint4*>(a.hout + row * a.K + e0) = *reinterpret_cast<const uint4*>(&raw[it][j]);
     }
   }
 
@@ -639,7 +683,7 @@ __global__ __launch_bounds__(kThreads) void row_quant_stream_kernel(RowArgs a) {
   const bool real = row < a.M;
   const int quad = wave * 16 + (lane >> 2);
   const int r = lane & 3;
-  const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.K;
+  const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.ldx;
   constexpr int NQ = 64;
   // The loop bound is uniform across the workgroup, so every lane runs the
   // same number of iterations and the DPP partners are always live.
@@ -831,6 +875,9 @@ int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float 
   a.scales = scales;
   a.zeros = zeros;
   a.sums = sums;
+  a.ldx = K;
+  a.up = nullptr;
+  a.hout = nullptr;
   const int esize = dtype == DSCQ_F16 ? 2 : 4;
   a.vec = (K % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
           ((K * esize) % 16 == 0);
@@ -860,6 +907,62 @@ int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float 
   }
   DSCQ_T(float)
 #undef DSCQ_T
+}
+
+// SiLU-gated activation quantization: rows h = silu(g) * u (fp16 roundings as
+// in silu_mul_f16x2) of g = gate[m, 0..N), u = up[m, 0..N), row stride ld
+// elements; the register kernel only (N <= 32768, 16-byte aligned rows).
+int silu_mul_quant(const void* gate, const void* up, int64_t ld, int64_t M, int64_t N,
+                   int64_t MP, float clip, int rotate_block, uint8_t* packed, float* scales,
+                   int32_t* zeros, void* hout, hipStream_t stream) {
+  RowArgs a;
+  a.x = gate;
+  a.up = up;
+  a.hout = static_cast<__half*>(hout);
+  a.ldx = ld;
+  a.M = M;
+  a.K = N;
+  a.KP = ceil_to(N, 64);
+  a.MP = MP;
+  a.nblk = (int)((a.KP + 127) / 128);
+  a.clip = clip;
+  a.qmax = 15.0f;
+  a.packed = packed;
+  a.codes = nullptr;
+  a.scales = scales;
+  a.zeros = zeros;
+  a.sums = nullptr;
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  a.vec = N % 8 == 0 && ld % 8 == 0 && al16(gate) && al16(up) && al16(hout);
+  int wpr, iters;
+  pick_shape(MP, a.nblk, &wpr, &iters);
+  if (!a.vec || wpr == 0)
+    return fail("silu_mul_quantize: need N %% 8 == 0, N <= 32768 and 16-byte aligned rows");
+  const int rows_per_wg = (kThreads / 64) / wpr;
+  const dim3 grid((unsigned)((a.MP + rows_per_wg - 1) / rows_per_wg));
+  const bool full = a.K == (int64_t)a.nblk * 128 && a.nblk == 16 * wpr * iters;
+#define DSCQ_GROWS(ROT, W, I)                                                                   \
+  if (wpr == W && iters == I) {                                                                 \
+    if (full)                                                                                   \
+      hipLaunchKernelGGL((row_quant_kernel<__half, ROT, kAct, W, I, true, true>), grid,         \
+                         dim3(kThreads), 0, stream, a);                                         \
+    else                                                                                        \
+      hipLaunchKernelGGL((row_quant_kernel<__half, ROT, kAct, W, I, false, true>), grid,        \
+                         dim3(kThreads), 0, stream, a);                                         \
+    return launch_status("row_quant_kernel");                                                  \
+  }
+#define DSCQ_GSHAPES(ROT)                                                                       \
+  DSCQ_GROWS(ROT, 1, 1) DSCQ_GROWS(ROT, 1, 2) DSCQ_GROWS(ROT, 1, 4)                             \
+  DSCQ_GROWS(ROT, 2, 1) DSCQ_GROWS(ROT, 2, 2) DSCQ_GROWS(ROT, 2, 4)                             \
+  DSCQ_GROWS(ROT, 4, 1) DSCQ_GROWS(ROT, 4, 2) DSCQ_GROWS(ROT, 4, 4)
+  if (rotate_block) {
+    DSCQ_GSHAPES(true)
+  } else {
+    DSCQ_GSHAPES(false)
+  }
+#undef DSCQ_GSHAPES
+#undef DSCQ_GROWS
+  return fail("internal: no row kernel for wpr=%d iters=%d", wpr, iters);
 }
 
 int pack_codes(const uint8_t* codes, uint8_t* packed, int64_t MP, int64_t KP,

@@ -25,8 +25,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["quantize", "matmul", "pack_weight", "padded", "check_quantize_args",
-           "check_matmul_args"]
+__all__ = ["quantize", "matmul", "pack_weight", "silu_mul_quantize", "padded",
+           "check_quantize_args", "check_matmul_args"]
 
 
 def padded(v: int, m: int) -> int:
@@ -170,3 +170,42 @@ def pack_weight(w: torch.Tensor, clip: float = 1.0, rotate_block: int = 0,
     if return_codes:
         return [packed, sw, sums, codes]
     return [packed, sw, sums]
+
+
+def silu_mul_quantize(gate_up: torch.Tensor, clip: float = 1.0, rotate_block: int = 0,
+                      return_h: bool = False):
+    """Quantize + pack the gated activation of a SiLU-gated MLP.
+
+    ``gate_up`` is the fp16 [M, 2N] output of one W4A4 GEMM against the
+    concatenated gate and up weights (gate in columns [0, N), up in [N, 2N)).
+    The rows quantized are h = fp16(fp16(silu(g)) * u), the down projection's
+    input; the result is what ``quantize(h, clip, True, rotate_block)`` returns:
+    [packed u8 [MP, KP/2], scales f32 [MP], zeros i32 [MP]] (KP = ceil64(N)),
+    plus h [M, N] fp16 when ``return_h``.
+    """
+    _check_cuda(gate_up)
+    if gate_up.dtype != torch.float16:
+        raise RuntimeError("silu_mul_quantize: gate|up must be fp16")
+    if gate_up.dim() != 2 or gate_up.size(1) % 2:
+        raise RuntimeError("silu_mul_quantize: expected [M, 2N]")
+    clip = float(clip)
+    if not (0.5 <= clip <= 1.0):
+        raise RuntimeError("Activation clip must be in [0.5,1]")
+    M, N = gate_up.size(0), gate_up.size(1) // 2
+    if rotate_block not in (0, 128) or (rotate_block and N % rotate_block):
+        raise RuntimeError(f"Rotation needs N to be a multiple of {rotate_block} (got N={N})")
+    dev = gate_up.device
+    _lib.require_gfx950(dev)
+    MP, KP = padded(M, 8), padded(N, 64)
+    packed = torch.empty((MP, KP // 2), dtype=torch.uint8, device=dev)
+    scales = torch.empty((MP,), dtype=torch.float32, device=dev)
+    zeros = torch.empty((MP,), dtype=torch.int32, device=dev)
+    h = torch.empty((M, N), dtype=torch.float16, device=dev) if return_h else None
+    with torch.cuda.device(dev):
+        _lib.call("dscq_silu_mul_quantize", gate_up.data_ptr(), gate_up.data_ptr() + 2 * N,
+                  2 * N, M, N, clip, rotate_block, packed.data_ptr(), scales.data_ptr(),
+                  zeros.data_ptr(), _lib.ptr(h), _lib.stream(dev))
+    out = [packed, scales, zeros]
+    if return_h:
+        out.append(h)
+    return out

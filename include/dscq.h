@@ -57,6 +57,26 @@ int dscq_quantize(const void* x, int x_dtype, int64_t M, int64_t K, float clip,
                   int32_t* zeros, uint8_t* codes, void* stream);
 
 /*
+ * Quantize + pack of the SiLU-gated activation between the up and down
+ * projections of a gated MLP (the caller of two QuantLinear layers in a
+ * Llama MLP: down(act_fn(gate(x)) * up(x)); core/model_ops.py drives such
+ * models, core/linear.py:48-52 quantizes the down projection's input).  The
+ * rows quantized are h = fp16(fp16(silu(g)) * u) with silu(g) = g / (1 + e^-g)
+ * in fp32 -- the two roundings an fp16 model applies -- then exactly as
+ * dscq_quantize(h, F16, M, N, clip, fused = 1, rotate_block).  No reference
+ * counterpart exists: the reference runs these ops unquantized in torch.
+ *   gate, up  fp16 rows [M, >= N] with row stride ld elements (e.g. the two
+ *             halves of one [M, 2N] gate|up GEMM output: up = gate + N,
+ *             ld = 2N); 16-byte aligned, N % 8 == 0 and ld % 8 == 0.
+ *   packed, scales, zeros  as dscq_quantize (MP = ceil(M/8)*8, KP = ceil(N/64)*64).
+ *   h         optional out fp16 [M, N]: the activation quantized (may be NULL).
+ * Limits: 1 <= M <= 65535, 1 <= N <= 32768.
+ */
+int dscq_silu_mul_quantize(const void* gate, const void* up, int64_t ld, int64_t M,
+                           int64_t N, float clip, int rotate_block, uint8_t* packed,
+                           float* scales, int32_t* zeros, void* h, void* stream);
+
+/*
  * Activation codes with any bit width 2..8 (no packing), the GPU form of
  * activation_codes (core/quantization.py:13-21) on the padded layout.
  *   codes  out u8 [MP, KP] in [0, 2^bits - 1] (padded k / rows: the row's zero)

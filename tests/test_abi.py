@@ -89,6 +89,12 @@ def test_c_other_argument_checks():
     assert "Weight clip" in _einval("dscq_pack_weight", d, 0, 4, 64, 1.5, 0, d, d, d, None, None)
     assert "bits" in _einval("dscq_weight_codes", d, 0, 4, 64, 1.0, 1, 0, d, d, None)
     assert "width" in _einval("dscq_unpack_int4", d, 2, 3, 7, d, None)
+    assert "N<=32768" in _einval("dscq_silu_mul_quantize", d, d, 40000, 4, 40000, 1.0, 0, d, d,
+                                 d, None, None)
+    assert "stride" in _einval("dscq_silu_mul_quantize", d, d, 8, 4, 16, 1.0, 0, d, d, d, None,
+                               None)
+    assert "multiple of 128" in _einval("dscq_silu_mul_quantize", d, d, 384, 4, 192, 1.0, 128,
+                                        d, d, d, None, None)
 
 
 # ------------------------------------------------------- Python-side messages

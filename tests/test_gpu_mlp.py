@@ -1,0 +1,108 @@
+"""SiLU-gated W4A4 MLP block on the GPU.
+
+The gated activation h = fp16(fp16(silu(g)) * u) depends on exp, whose last
+bit differs between the GPU's and the CPU's libraries, so h is checked
+against torch's CPU fp16 composition within one fp16 ulp.  Everything after
+h is integer or fixed-order fp32 and is checked bit for bit against the
+oracle applied to the kernel's own h: packed codes, scales and zero-points of
+the down projection's input (with its online rotation) and the block output.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from dscquant_amd import w4a4
+from dscquant_amd.core.linear import QuantLinear
+from dscquant_amd.core.mlp import QuantMLP
+from oracle import native
+from tests.conftest import activations, weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _h_reference(gu: torch.Tensor) -> torch.Tensor:
+    """An fp16 model's act_fn(gate) * up on the CPU."""
+    N = gu.shape[1] // 2
+    g, u = gu[:, :N].cpu(), gu[:, N:].cpu()
+    return F.silu(g.float()).half() * u
+
+
+@pytest.mark.parametrize("M,N,rot", [(1, 512, 0), (16, 11008, 128), (37, 1024, 128),
+                                     (512, 11008, 128), (64, 640, 0)])
+def test_silu_mul_quantize_matches_oracle(gpu, M, N, rot):
+    print(f"silu_mul_quantize case M{M} N{N} rot{rot}", flush=True)
+    g = torch.Generator().manual_seed(M + N)
+    gu = (torch.randn(M, 2 * N, generator=g) * 2.0).half().to(gpu)
+    packed, sx, zx, h = w4a4.silu_mul_quantize(gu, 1.0, rot, return_h=True)
+    torch.cuda.synchronize()
+    h_ref = _h_reference(gu)
+    hk = h.cpu()
+    ulp = torch.maximum(hk.float().abs(), torch.tensor(6.1e-5)) * 2.0 ** -10
+    assert ((hk.float() - h_ref.float()).abs() <= ulp).all()
+    # codes of the kernel's own h: bit-exact against the oracle
+    pa, sx_ref, zx_ref = native.quantize_rows(hk.float().numpy(), 1.0, rot)
+    np.testing.assert_array_equal(packed.cpu().numpy(), pa)
+    np.testing.assert_array_equal(sx.cpu().numpy(), sx_ref)
+    np.testing.assert_array_equal(zx.cpu().numpy(), zx_ref)
+    # without the h output the kernel writes the same codes
+    p2, s2, z2 = w4a4.silu_mul_quantize(gu, 1.0, rot)
+    assert torch.equal(p2, packed) and torch.equal(s2, sx) and torch.equal(z2, zx)
+
+
+class Cfg:
+    weight_bits = 4
+    activation_bits = 4
+
+
+def _linear(n_out, n_in, seed, gpu, bias=False):
+    lin = torch.nn.Linear(n_in, n_out, bias=bias)
+    with torch.no_grad():
+        lin.weight.copy_(torch.from_numpy(weights(n_out, n_in, seed=seed).astype(np.float32)))
+        if bias:
+            lin.bias.copy_(torch.randn(n_out, generator=torch.Generator().manual_seed(seed)) * 0.1)
+    return lin.half().to(gpu)
+
+
+@pytest.mark.parametrize("M,K,N,bias", [(16, 1024, 2816, False), (128, 4096, 11008, False),
+                                        (40, 512, 1024, True)])
+def test_quant_mlp_matches_oracle(gpu, M, K, N, bias):
+    print(f"QuantMLP case M{M} K{K} N{N} bias{bias}", flush=True)
+    gate = QuantLinear(_linear(N, K, 1, gpu, bias), Cfg())
+    up = QuantLinear(_linear(N, K, 2, gpu, bias), Cfg())
+    down = QuantLinear(_linear(K, N, 3, gpu, bias), Cfg())
+    for m in (gate, up, down):
+        m.enabled = True
+    down.rotate_block = 128
+    mlp = QuantMLP(gate, up, down)
+    x = torch.from_numpy(activations(M, K, seed=7)).to(gpu)
+    with torch.no_grad():
+        y = mlp(x)
+    torch.cuda.synchronize()
+    assert y.shape == (M, K) and y.dtype == torch.float16
+
+    # the same chain through the oracle, starting from the kernel's own h
+    xf = x.float().cpu().numpy()
+    wg, wu, wd = (m.base.weight.float().cpu().numpy() for m in (gate, up, down))
+    bgu = (np.concatenate([gate.base.bias.cpu().numpy(), up.base.bias.cpu().numpy()])
+           if bias else None)
+    gu_ref, *_ = native.linear_w4a4(xf, np.concatenate([wg, wu]), bgu)
+    pa, sx, zx = w4a4.quantize(x, 1.0, True, 0)
+    pgu, swgu, sgu, bgu_t, *_ = mlp.packed()
+    gu, _ = w4a4.matmul(pa, pgu, sx, zx, swgu, sgu,
+                        bgu_t if bgu_t is not None else torch.empty(0, dtype=torch.float16,
+                                                                    device=gpu),
+                        M, 2 * N, True, False, False)
+    np.testing.assert_array_equal(gu.cpu().numpy(), gu_ref)
+    _, _, _, h = w4a4.silu_mul_quantize(gu, 1.0, 128, return_h=True)
+    bd = down.base.bias.cpu().numpy() if bias else None
+    y_ref, *_ = native.linear_w4a4(h.float().cpu().numpy(), wd, bd, rotate_block=128)
+    np.testing.assert_array_equal(y.cpu().numpy(), y_ref)
+
+    # tolerance against the unquantized fp32 block (W4A4 error, not a parity bar)
+    with torch.no_grad():
+        xf_t = x.float().cpu()
+        ref = F.linear(F.silu(F.linear(xf_t, torch.from_numpy(wg))) *
+                       F.linear(xf_t, torch.from_numpy(wu)), torch.from_numpy(wd))
+    rel = (y.float().cpu() - ref).norm() / ref.norm()
+    assert rel < 0.5, rel

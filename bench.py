@@ -47,6 +47,9 @@ WORKLOADS = {
     "mlp_up": (512, 11008, 4096, 128),
     "mlp_down": (512, 4096, 11008, 128),
     "70b_qo": (4096, 8192, 8192, 128),
+    # SiLU-gated MLP block (Llama-7B shapes): x[M,K] -> gate|up GEMM [M, 2N] ->
+    # silu*up + rotate + quantize -> down GEMM [M, K]
+    "mlp": (512, 11008, 4096, 128),
 }
 
 
@@ -195,6 +198,9 @@ def main():
 
     import torch
     from dscquant_amd import _lib, w4a4
+
+    if args.workload == "mlp":
+        return main_mlp(args, torch, _lib, w4a4)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -354,6 +360,141 @@ def main():
             "gemm": gemm_line,
         },
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(result))
+
+
+def run_graph_steps(args, torch, dev, step):
+    """Whole-step timing: runs of up to 64 steps captured per HIP graph."""
+    GRAPH_STEPS = 64
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for i in range(3):
+            step(i)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+
+    def plan(n):
+        out = []
+        full, rest = divmod(n, GRAPH_STEPS)
+        for count, reps in ((GRAPH_STEPS, full), (rest, 1)):
+            if count and reps:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for i in range(count):
+                        step(i)
+                out.append((g, reps))
+        torch.cuda.synchronize()
+        return out
+
+    def run(graphs):
+        for g, reps in graphs:
+            for _ in range(reps):
+                g.replay()
+
+    run(plan(args.warmup))
+    timed = plan(args.steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run(timed)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / args.steps
+
+
+def main_mlp(args, torch, _lib, w4a4):
+    """The SiLU-gated MLP block: four launches per step."""
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.require_gfx950(dev)
+    M, N, K, rot = WORKLOADS["mlp"]
+    MP, KP, NKP = (M + 7) // 8 * 8, (K + 63) // 64 * 64, (N + 63) // 64 * 64
+    x, wg = synthetic(M, N, K)
+    wu = (torch.randn(N, K, generator=torch.Generator().manual_seed(11)) * 0.02).half()
+    wd = (torch.randn(K, N, generator=torch.Generator().manual_seed(12)) * 0.02).half()
+    nbuf = max(2, math.ceil(2 * MALL_BYTES / (M * K * 2)))
+    xs = [x.to(dev)]
+    for i in range(1, nbuf):
+        xs.append(xs[0].roll(i, dims=0).contiguous())
+    pg, swg, sg = w4a4.pack_weight(wg.to(dev), 1.0, 0)
+    pu, swu, su = w4a4.pack_weight(wu.to(dev), 1.0, 0)
+    pgu, swgu, sgu = torch.cat([pg, pu]), torch.cat([swg, swu]), torch.cat([sg, su])
+    pd, swd, sd = w4a4.pack_weight(wd.to(dev), 1.0, rot)
+    pa = torch.empty((MP, KP // 2), dtype=torch.uint8, device=dev)
+    sx = torch.empty((MP,), dtype=torch.float32, device=dev)
+    zx = torch.empty((MP,), dtype=torch.int32, device=dev)
+    gu = torch.empty((M, 2 * N), dtype=torch.float16, device=dev)
+    ph = torch.empty((MP, NKP // 2), dtype=torch.uint8, device=dev)
+    sh = torch.empty((MP,), dtype=torch.float32, device=dev)
+    zh = torch.empty((MP,), dtype=torch.int32, device=dev)
+    out = torch.empty((M, K), dtype=torch.float16, device=dev)
+    L = _lib.lib()
+
+    def ok(rc):
+        assert rc == 0, L.dscq_last_error()
+
+    def quantize(i):
+        ok(L.dscq_quantize(xs[i % nbuf].data_ptr(), _lib.F16, M, K, 1.0, 1, 0, pa.data_ptr(),
+                           sx.data_ptr(), zx.data_ptr(), None, _lib.stream(dev)))
+
+    def gemm_gu(i):
+        ok(L.dscq_matmul(pa.data_ptr(), pgu.data_ptr(), sx.data_ptr(), zx.data_ptr(),
+                         swgu.data_ptr(), sgu.data_ptr(), None, M, 2 * N, KP, 1, 0, 0,
+                         gu.data_ptr(), None, _lib.stream(dev)))
+
+    def gated(i):
+        ok(L.dscq_silu_mul_quantize(gu.data_ptr(), gu.data_ptr() + 2 * N, 2 * N, M, N, 1.0, rot,
+                                    ph.data_ptr(), sh.data_ptr(), zh.data_ptr(), None,
+                                    _lib.stream(dev)))
+
+    def gemm_down(i):
+        ok(L.dscq_matmul(ph.data_ptr(), pd.data_ptr(), sh.data_ptr(), zh.data_ptr(),
+                         swd.data_ptr(), sd.data_ptr(), None, M, K, NKP, 1, 0, 0,
+                         out.data_ptr(), None, _lib.stream(dev)))
+
+    def step(i):
+        quantize(i)
+        gemm_gu(i)
+        gated(i)
+        gemm_down(i)
+
+    step(0)
+    torch.cuda.synchronize()
+    t = {name: time_kernel(fn, args.kernel_iters, torch, dev)
+         for name, fn in (("quantize", quantize), ("gemm_gate_up", gemm_gu),
+                          ("silu_mul_quantize", gated), ("gemm_down", gemm_down))}
+    sec = run_graph_steps(args, torch, dev, step)
+    ops = 2.0 * M * (2 * N) * K + 2.0 * M * K * N
+    gu_ops = 2.0 * M * (2 * N) * K
+    qbytes = 2 * M * K + M * KP // 2 + 8 * M
+    gbytes = 4 * M * N + M * NKP // 2 + 8 * M  # read gate|up fp16, write int4 + meta
+    line = {"bound": "mfma", "achieved": round(gu_ops / t["gemm_gate_up"] / 1e12, 2),
+            "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+            "frac": round(gu_ops / t["gemm_gate_up"] / 1e12 / PEAK_INT8_TOPS, 4),
+            "kernel": "w4a4_gemm_pipe_kernel (gate|up)", "avg_us": round(t["gemm_gate_up"] * 1e6, 3),
+            "ops_per_launch": gu_ops, "traffic": None}
+    result = {
+        "metric": METRIC, "value": round(ops / sec / 1e12, 2), "unit": "TOPS", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int4xint4->int32 (int8 MFMA), fp16 in/out",
+        "data": "synthetic: X~N(0,1) fp16 with 1% outlier channels x50, W~N(0,0.02), seeded",
+        "config": {"workload": f"mlp: SiLU-gated W4A4 MLP block M={M} K={K} N={N}, gate|up as "
+                               f"one GEMM, rotate_block={rot} on the down projection input",
+                   "M": M, "N": N, "K": K, "rotate_block": rot},
+        "roofline": line,
+        "kernels": {
+            "quantize": {"bound": "hbm", "avg_us": round(t["quantize"] * 1e6, 3),
+                         "achieved": round(qbytes / t["quantize"] / 1e9, 1), "unit": "GB/s"},
+            "gemm_gate_up": dict(line),
+            "silu_mul_quantize": {"bound": "hbm", "avg_us": round(t["silu_mul_quantize"] * 1e6, 3),
+                                  "achieved": round(gbytes / t["silu_mul_quantize"] / 1e9, 1),
+                                  "unit": "GB/s"},
+            "gemm_down": {"bound": "mfma", "avg_us": round(t["gemm_down"] * 1e6, 3),
+                          "achieved": round(2.0 * M * K * N / t["gemm_down"] / 1e12, 2),
+                          "unit": "TOPS"},
+        },
+        "cpu_baseline": None,
     }
     print(json.dumps(result))
 

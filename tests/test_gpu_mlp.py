@@ -2,7 +2,8 @@
 
 The gated activation h = fp16(fp16(silu(g)) * u) depends on exp, whose last
 bit differs between the GPU's and the CPU's libraries, so h is checked
-against torch's CPU fp16 composition within one fp16 ulp.  Everything after
+against torch's CPU fp16 composition within a few fp16 ulps (and equal on
+more than 99% of the elements).  Everything after
 h is integer or fixed-order fp32 and is checked bit for bit against the
 oracle applied to the kernel's own h: packed codes, scales and zero-points of
 the down projection's input (with its online rotation) and the block output.
@@ -38,8 +39,11 @@ def test_silu_mul_quantize_matches_oracle(gpu, M, N, rot):
     torch.cuda.synchronize()
     h_ref = _h_reference(gu)
     hk = h.cpu()
-    ulp = torch.maximum(hk.float().abs(), torch.tensor(6.1e-5)) * 2.0 ** -10
-    assert ((hk.float() - h_ref.float()).abs() <= ulp).all()
+    # A last-bit exp difference can flip the fp16 rounding of silu(g), which
+    # the product carries into h as up to ~2.5 fp16 ulps; exact elsewhere.
+    diff = (hk.float() - h_ref.float()).abs()
+    assert (diff <= torch.maximum(hk.float().abs(), torch.tensor(6.1e-5)) * 2.0 ** -8).all()
+    assert (diff == 0).float().mean() > 0.99
     # codes of the kernel's own h: bit-exact against the oracle
     pa, sx_ref, zx_ref = native.quantize_rows(hk.float().numpy(), 1.0, rot)
     np.testing.assert_array_equal(packed.cpu().numpy(), pa)

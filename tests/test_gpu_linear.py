@@ -83,3 +83,52 @@ def test_quant_linear_other_bit_widths_use_gpu_codes(gpu):
     wq = fakequant.quantize_weight(w, 8)
     ref = torch.nn.functional.linear(xa, wq, layer.base.bias.detach().cpu())
     torch.testing.assert_close(y.cpu(), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_quant_linear_w4a4_with_learned_transforms(gpu):
+    """Folds of core/linear.py:22-46 (per-head rotation on the o projection, diagonal
+    scaling on up / down) on the integer path: the module's folded weight agrees with
+    the fold formula in fp32 tolerance (matmul order is the device's), and the output
+    is bit-exact against the oracle fed that same folded weight."""
+
+    class Rot(torch.nn.Module):
+        def __init__(self, heads, head_dim):
+            super().__init__()
+            self.heads, self.head_dim = heads, head_dim
+            q, _ = torch.linalg.qr(torch.randn(heads, head_dim, head_dim,
+                                               generator=torch.Generator().manual_seed(5)))
+            self.m = q.to(gpu)
+
+        def matrices(self):
+            return self.m
+
+    class Scl(torch.nn.Module):
+        def __init__(self, n):
+            super().__init__()
+            self.s = (torch.rand(n, generator=torch.Generator().manual_seed(6)) + 0.5).to(gpu)
+
+        def diagonal(self):
+            return self.s
+
+    M = 24
+    cases = [(Rot(8, 64), "o", 512, 512), (Scl(1024), "up", 1024, 512), (Scl(512), "down", 256, 512)]
+    for interface, role, N, K in cases:
+        print(f"QuantLinear fold case role {role} N{N} K{K}", flush=True)
+        layer = QuantLinear(_layer(N, K, gpu, bias=False), Cfg(), interface, role)
+        layer.enabled = True
+        x = torch.from_numpy(activations(M, K, seed=8)).to(gpu)
+        with torch.no_grad():
+            y = layer(x)
+        w_fold, _ = layer.transformed()
+        w0 = layer.base.weight.float()
+        if role == "o":
+            R = interface.m.float()
+            ref = torch.einsum("ohd,hde->ohe", w0.reshape(N, 8, 64), R).reshape(N, K)
+        elif role == "up":
+            ref = w0 / interface.s[:, None]
+        else:
+            ref = w0 * interface.s[None, :]
+        torch.testing.assert_close(w_fold.float(), ref.half().float(), rtol=2e-3, atol=2e-5)
+        out_ref, *_ = native.linear_w4a4(x.float().cpu().numpy(),
+                                         w_fold.float().cpu().numpy(), None)
+        np.testing.assert_array_equal(y.cpu().numpy(), out_ref)

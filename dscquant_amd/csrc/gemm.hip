@@ -329,19 +329,20 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   const int nslices = (int)((KB + SB - 1) / SB);
 
   // Global pieces of this thread: unit u = tid % UNITS of rows
-  // tid / UNITS + (THREADS / UNITS) i.  Rows past MP / NP are clamped (never stored).
+  // tid / UNITS + (THREADS / UNITS) i -- rows of A for i < BM / (THREADS / UNITS),
+  // of B after.  Rows past MP / NP are clamped (never stored).  Offsets are
+  // 32-bit (the launcher checks rows * KB < 2^32), so every load is the
+  // scalar-base + 32-bit vector-offset form: no 64-bit address arithmetic per
+  // load, measurably cheaper in the K loop.
+  static_assert(BM % (THREADS / UNITS) == 0, "a piece index is all-A or all-B");
+  constexpr int A_PIECES = BM / (THREADS / UNITS);
   const int u = tid % UNITS;
-  const uint8_t* src[LOADS];
+  uint32_t src_off[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
     const int R = tid / UNITS + (THREADS / UNITS) * i;
-    if (R < BM) {
-      const int64_t row = min(m0 + R, g.arows - 1);
-      src[i] = g.a + row * KB + u * 16;
-    } else {
-      const int64_t row = min(n0 + (R - BM), g.brows - 1);
-      src[i] = g.b + row * KB + u * 16;
-    }
+    const int64_t row = i < A_PIECES ? min(m0 + R, g.arows - 1) : min(n0 + (R - BM), g.brows - 1);
+    src_off[i] = (uint32_t)(row * KB + u * 16);
   }
   // (R >> 1) & 7 depends on tid only: THREADS / UNITS is a multiple of 16.
   const int wr_off = (tid / UNITS) * SB + 16 * (u ^ ((tid / UNITS >> 1) & 7));
@@ -355,7 +356,8 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     if (KTAIL && tail) kb = KB - 16 - u * 16;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      uint4 v = *reinterpret_cast<const uint4*>(src[i] + kb);
+      const uint8_t* base = i < A_PIECES ? g.a : g.b;
+      uint4 v = *reinterpret_cast<const uint4*>(base + (src_off[i] + (uint32_t)kb));
       if (KTAIL && tail) v = make_uint4(0u, 0u, 0u, 0u);
       st[i] = v;
     }
@@ -709,7 +711,9 @@ int launch_gemv(GemmArgs g, hipStream_t stream) {
 // aligned output and raw rows, 64+ rows.
 bool pipe_ok(const GemmArgs& g) {
   auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
-  return g.N % 8 == 0 && g.M >= 64 && al(g.out, 16) && al(g.raw, 16);
+  const int64_t KB = g.KP / 2;
+  return g.N % 8 == 0 && g.M >= 64 && al(g.out, 16) && al(g.raw, 16) &&
+         g.arows * KB <= 0xFFFFFFFFll && g.brows * KB <= 0xFFFFFFFFll;
 }
 
 // DSCQ_GEMM_TILE=<BM>x<BN>[w8] pins the tile shape (tuning sweeps only).

@@ -34,12 +34,10 @@
 
 #include "../../include/dscq.h"
 #include "common.h"
+#include "mma_int4.h"
 
 namespace dscq {
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 
 struct GemmArgs {
   const uint8_t* a;
@@ -58,31 +56,6 @@ struct GemmArgs {
 
 constexpr int kSliceBytes = 64;  // 128 nibbles of K per LDS stage
 constexpr int kPlanePad = 64;
-
-__device__ __forceinline__ v4i unpack8(uint32_t w0, uint32_t w1) {
-  v4i r;
-  r[0] = (int)((w0 << 4) & 0xF0F0F0F0u);
-  r[1] = (int)(w0 & 0xF0F0F0F0u);
-  r[2] = (int)((w1 << 4) & 0xF0F0F0F0u);
-  r[3] = (int)(w1 & 0xF0F0F0F0u);
-  return r;
-}
-
-template <typename OutT>
-__device__ __forceinline__ OutT to_out(float v);
-// The reference rounds the fp32 result, then narrows it to fp16 (two
-// roundings).  Left alone, the compiler folds a preceding fp32 multiply / add
-// into the narrowing (v_fma_mixlo_f16: one rounding), which differs on exact
-// fp16 ties; the empty asm pins the fp32 value first.
-template <>
-__device__ __forceinline__ __half to_out<__half>(float v) {
-  asm("" : "+v"(v));
-  return __float2half_rn(v);
-}
-template <>
-__device__ __forceinline__ float to_out<float>(float v) {
-  return v;
-}
 
 template <typename OutT, int BM, int BN, int WM, int WN, bool HUGE>
 __global__ __launch_bounds__(64 * WM * WN) void w4a4_gemm_kernel(GemmArgs g) {

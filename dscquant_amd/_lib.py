@@ -31,6 +31,8 @@ SIGNATURES = {
     "dscq_pack_weight": [_P, _I, _I64, _I64, _F, _I, _P, _P, _P, _P, _P],
     "dscq_weight_codes": [_P, _I, _I64, _I64, _F, _I, _I, _P, _P, _P],
     "dscq_matmul": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P, _P],
+    "dscq_linear_decode": [_P, _I, _I64, _I64, _F, _I, _P, _P, _P, _P, _I64, _I, _P, _P],
+    "dscq_linear_decode_supported": [_I64, _I64],
     "dscq_pack_int4": [_P, _I64, _I64, _P, _P],
     "dscq_unpack_int4": [_P, _I64, _I64, _I64, _P, _P],
     "dscq_device_supported": [],

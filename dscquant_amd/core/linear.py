@@ -125,6 +125,12 @@ class QuantLinear(nn.Module):
              else bias.detach().to(out_dtype).contiguous())
         aclip = float(self.activation_clip.detach().float().item())
         M = xr.shape[0]
+        if (M > 0 and xr.data_ptr() % 16 == 0
+                and w4a4.linear_decode_supported(M, K)):
+            # A few tokens: quantize and multiply in one launch (bit-identical).
+            out = w4a4.linear_decode(xr, aclip, int(self.rotate_block), packed_w, sw, sums, b,
+                                     N, fp32)
+            return out.reshape(*lead, N).to(x.dtype)
         out = torch.empty((M, N), dtype=out_dtype, device=x.device)
         for r0 in range(0, max(M, 1), _MAX_ROWS):
             part = xr[r0:r0 + _MAX_ROWS]

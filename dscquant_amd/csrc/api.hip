@@ -27,6 +27,10 @@ int w4a4_gemm(const uint8_t* a, const uint8_t* b, const float* sx, const int32_t
               const float* sw, const int32_t* sums, const void* bias, int64_t M,
               int64_t N, int64_t KP, bool decode, bool out_fp32, void* out,
               int32_t* raw, hipStream_t stream);
+bool linear_decode_fits(int64_t M, int64_t K);
+int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, int rotate_block,
+                  const uint8_t* b, const float* sw, const int32_t* sums, const void* bias,
+                  int64_t N, bool out_fp32, void* out, hipStream_t stream);
 
 namespace {
 thread_local char g_last_error[512] = "";
@@ -103,6 +107,26 @@ int dscq_quantize(const void* x, int x_dtype, int64_t M, int64_t K, float clip, 
     return rc;
   return pack_codes(codes, packed, MP, KP, s);
 }
+
+int dscq_linear_decode(const void* x, int x_dtype, int64_t M, int64_t K, float clip,
+                       int rotate_block, const uint8_t* b, const float* sw,
+                       const int32_t* sums, const void* bias, int64_t N, int out_fp32,
+                       void* out, void* stream) {
+  if (!valid_dtype(x_dtype)) return fail("Only FP16 and FP32 inputs are supported");
+  if (!linear_decode_fits(M, K))
+    return fail("linear_decode: M=%lld, K=%lld exceed the fused decode kernel (quantize + "
+                "matmul instead)", (long long)M, (long long)K);
+  if (!(N > 0 && N <= 0x7FFFFFFFLL)) return fail("Invalid dimensions");
+  if (!(clip >= 0.5f && clip <= 1.0f)) return fail("Activation clip must be in [0.5,1]");
+  if (int rc = check_rotation(rotate_block, K)) return rc;
+  if (!x || !b || !sw || !sums || !out) return fail("linear_decode: null buffer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0)
+    return fail("linear_decode: x must be 16-byte aligned");
+  return linear_decode(x, x_dtype, M, K, clip, rotate_block, b, sw, sums, bias, N,
+                       out_fp32 != 0, out, static_cast<hipStream_t>(stream));
+}
+
+int dscq_linear_decode_supported(int64_t M, int64_t K) { return linear_decode_fits(M, K) ? 1 : 0; }
 
 int dscq_silu_mul_quantize(const void* gate, const void* up, int64_t ld, int64_t M,
                            int64_t N, float clip, int rotate_block, uint8_t* packed,

@@ -1,0 +1,376 @@
+// Fused decode linear for gfx950: activation quantize (+ online rotation) and
+// the skinny-M W4A4 product in one launch.
+//
+// For a handful of tokens the two-launch path (quantize, then the skinny-M
+// GEMM) is latency-bound: each kernel is a few microseconds of launch and
+// first-byte latency around well under a microsecond of work.  Here every
+// workgroup owns 16 output columns, as in the skinny-M GEMM, and
+//   1. issues the loads of its activation blocks and, right behind them, of
+//      its whole weight stripe (16 rows of b, all of K), so the HBM stream
+//      starts at once;
+//   2. quantizes all M activation rows itself -- the same per-element
+//      arithmetic as the quantize kernel (rowquant.h), so codes, scales and
+//      zero-points are bit-identical -- into LDS, while the weights arrive;
+//   3. runs the int8-MFMA dot products from LDS and registers and applies the
+//      reference's epilogue (kernel/w4a4.cu:70-78, 156-161).
+// The quantization is repeated by every workgroup; it is cheap only while
+// M * ceil(K / 128) <= 128 (one 128-element block per quad of lanes), which
+// is the limit this kernel accepts (decode: M <= 4 at K = 4096, M = 1 up to
+// K = 12288).  Larger inputs take the two-launch path.
+//
+// Result: out == matmul(quantize(x, clip, fused, rotate_block), b, ...) of
+// the reference extension (kernel/w4a4.cu:164-225), bit for bit.
+
+#include <cstdlib>
+
+#include "../../include/dscq.h"
+#include "common.h"
+#include "mma_int4.h"
+#include "rowquant.h"
+
+namespace dscq {
+namespace {
+
+constexpr int kWaves = 8;                 // workgroup = 8 waves = 32 blocks of 16 lanes
+constexpr int kMaxBlocks = 128;           // activation blocks (M * nblk)
+constexpr int kMaxBlocksPerWave = 12;     // 64-byte k blocks of b per wave (max)
+constexpr int kMaxABytes = 16384;         // LDS for the packed activations
+
+struct DecodeArgs {
+  const void* x;          // [M, K] fp16 / fp32, rows 16-byte aligned
+  int64_t M, K, KP, KB;   // KB = KP / 2 bytes per packed row
+  int nblk;               // ceil(KP / 128)
+  float clip;
+  const uint8_t* b;       // [>= NP, KB]
+  int64_t brows;          // NP
+  const float* sw;
+  const int32_t* sums;
+  const void* bias;       // [N] of the output type, or null
+  int64_t N;
+  void* out;              // [M, N]
+};
+
+// Cross-lane butterfly through the LDS crossbar (ds_swizzle, no memory):
+// partner = lane ^ XOR within 32 lanes; the lane whose XOR bit is clear keeps
+// own + partner, the other partner - own -- fma(+-1, own, partner), rounded
+// exactly like the plain add / subtract.
+template <int XOR>
+__device__ __forceinline__ void bfly_swizzle(float (&c)[8], float sgn) {
+  constexpr int kPattern = 0x1F | (XOR << 10);  // bit mode: and 0x1f, xor XOR
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float p = __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, c[i]), kPattern));
+    c[i] = __builtin_fmaf(sgn, c[i], p);
+  }
+}
+
+// PER: weight blocks held per wave (4, 8 or 12 >= the blocks a wave owns),
+// a compile-time count so the loads are unconditional -- a load behind a
+// branch makes the wait for an earlier load conservative.
+//
+// Activation layouts (both run the quantize kernel's butterflies in the same
+// order, so every value is rounded identically; rowquant.h):
+//   SPREAD (ITERS = 1 or 2 passes of 32 blocks, M * nblk <= 64): a 128-element
+//     block over 16 consecutive lanes, lane 4j + r holding elements
+//     j*32 + r*8 .. +7 (one 16-byte load).  Index bits 0-2 in the lane, bits
+//     3-4 (r) across the quad by DPP (sign-folded: lanes r = 1, 2 end up
+//     holding -y), bits 5-6 (j) across quads by ds_swizzle xor 4 / xor 8
+//     (pairs share r, hence the sign).  8 elements per lane per pass.
+//   QUAD (ITERS = 0, M * nblk <= 128): the quantize kernel's layout, a block
+//     per quad of lanes, 32 elements per lane, bits 5-6 in the lane.
+template <typename T, typename OutT, bool ROT, bool BIAS, int PER, int ITERS>
+__global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) {
+  constexpr bool QUAD = ITERS == 0;
+  constexpr int NCH = QUAD ? 4 : ITERS;  // 8-element chunks per lane
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[kMaxABytes];
+  __shared__ int32_t part[kWaves][16][16];
+  __shared__ float bmin[kMaxBlocks], bmax[kMaxBlocks];
+  __shared__ float rmin[kWaves], rmax[kWaves];
+  __shared__ float rsx[kWaves];
+  __shared__ int32_t rzx[kWaves];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int r = lane & 15, grp = lane >> 4;
+
+  // ---- 1a. activations.  Chunk c of this lane: block slot g[c] (row
+  // g / nblk, block g % nblk), 32-element group jj[c], quad lane qr.
+  const int qr = lane & 3;
+  int g[NCH], jj[NCH];
+  bool ok[NCH];
+  Raw<T> raw[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    g[c] = QUAD ? (tid >> 2) : c * 32 + (tid >> 4);
+    jj[c] = QUAD ? c : (lane >> 2) & 3;
+    const int row = g[c] / d.nblk, blk = g[c] % d.nblk;
+    const bool live = row < d.M;
+    const int64_t e0 = (int64_t)blk * 128 + jj[c] * 32 + qr * 8;
+    ok[c] = live && e0 < d.K;
+    const T* xrow = static_cast<const T*>(d.x) + (live ? row : 0) * d.K;
+    raw[c] = load_raw<T>(xrow, e0, ok[c]);
+  }
+
+  // ---- 1b. the weight stripe, issued right after the activation loads (a
+  // wave's loads complete in issue order, so the activations are not queued
+  // behind the weights): lane (r, grp) holds 16 bytes of row n0 + r at
+  // byte 16 * grp of each of the wave's 64-byte blocks.
+  const int64_t nkb = (d.KB + 63) / 64;
+  const int64_t per = (nkb + kWaves - 1) / kWaves;
+  const int64_t b0 = wave * per;
+  const uint8_t* brow = d.b + min(n0 + r, d.brows - 1) * d.KB;
+  const int64_t off = grp * 16;
+  // Pieces past the wave's blocks or the row end (the last block of a row
+  // with KB % 64 == 32 is half empty) re-read the row's last piece and are
+  // zeroed where they are used: overwriting a load's destination here would
+  // wait for the load.
+  uint4 bv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t kb = (b0 + i) * 64;
+    const bool in = i < per && kb + off < d.KB;
+    bv[i] = *reinterpret_cast<const uint4*>(brow + (in ? kb + off : d.KB - 16));
+  }
+  // Keep every load above the arithmetic (the scheduler would otherwise sink
+  // the weight loads below the transform to save registers).
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 2. rotate + quantize the activations into LDS.  Blocks past the M
+  // rows work on row 0's data and their results are never read.  Elements
+  // past K (only without rotation: it needs K % 128 == 0) are zeroed after
+  // the conversion; masking the raw load results instead turns the loads
+  // into branches issued behind the weight stripe.
+  float v[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (ROT && sizeof(T) == 2) {
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(&raw[c]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) bfly_f16x2(w[k], v[c][2 * k], v[c][2 * k + 1]);
+      fwht_chunk_tail(v[c]);
+    } else {
+      to_f32(raw[c], v[c]);
+      if (ROT) fwht_chunk(v[c]);
+      else mask_f32<T>(ok[c], v[c]);
+    }
+  }
+  if (ROT) {
+    if constexpr (QUAD) {
+      fwht_block_tail_signed(v, qr);
+    } else {
+      const float s1 = (qr & 1) ? -1.0f : 1.0f, s2 = (qr & 2) ? -1.0f : 1.0f;
+      const float s4 = (lane & 4) ? -1.0f : 1.0f, s8 = (lane & 8) ? -1.0f : 1.0f;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        fmac_dpp_xor1(v[c], s1);
+        fmac_dpp_xor2(v[c], s2);
+        bfly_swizzle<4>(v[c], s4);
+        bfly_swizzle<8>(v[c], s8);
+      }
+    }
+  }
+  const float lsign = (ROT && (qr == 1 || qr == 2)) ? -1.0f : 1.0f;
+  // Block min / max (with 0, as lo = min(x, 0), hi = max(x, 0)), sign undone,
+  // then over the block's lanes (a quad, or 16 lanes).
+  auto block_minmax = [&](float mn, float mx, int slot, bool writer) {
+    if (ROT && lsign < 0.0f) {
+      const float t = mn;
+      mn = -mx;
+      mx = -t;
+    }
+    mn = fminf(mn, dpp_f32<kDppQuadXor1>(mn));
+    mx = fmaxf(mx, dpp_f32<kDppQuadXor1>(mx));
+    mn = fminf(mn, dpp_f32<kDppQuadXor2>(mn));
+    mx = fmaxf(mx, dpp_f32<kDppQuadXor2>(mx));
+    if (!QUAD) {
+      mn = fminf(mn, dpp_f32<kDppRowRor4>(mn));
+      mx = fmaxf(mx, dpp_f32<kDppRowRor4>(mx));
+      mn = fminf(mn, dpp_f32<kDppRowRor8>(mn));
+      mx = fmaxf(mx, dpp_f32<kDppRowRor8>(mx));
+    }
+    if (writer) {
+      bmin[slot] = mn;
+      bmax[slot] = mx;
+    }
+  };
+  if constexpr (QUAD) {
+    float mn = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        mn = fminf(mn, v[c][i]);
+        mx = fmaxf(mx, v[c][i]);
+      }
+    block_minmax(mn, mx, g[0], qr == 0);
+  } else {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      float mn = 0.0f, mx = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        mn = fminf(mn, v[c][i]);
+        mx = fmaxf(mx, v[c][i]);
+      }
+      block_minmax(mn, mx, g[c], r == 0);
+    }
+  }
+  __syncthreads();
+  // Row statistics: wave w < M reduces row w's nblk (<= 128) block entries.
+  if (wave < d.M) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = lane + 64 * h;
+      if (e < d.nblk) {
+        a0 = fminf(a0, bmin[wave * d.nblk + e]);
+        a1 = fmaxf(a1, bmax[wave * d.nblk + e]);
+      }
+    }
+    a0 = wave_min(a0);
+    a1 = wave_max(a1);
+    if (lane == 0) {
+      rmin[wave] = a0;
+      rmax[wave] = a1;
+    }
+  }
+  __syncthreads();
+  const bool noclamp = d.clip == 1.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int row = g[c] / d.nblk, blk = g[c] % d.nblk;
+    if (row < d.M) {
+      const RowScale rs = row_scale<kAct>(rmin[row], rmax[row], d.clip, 15.0f);
+      RowScale rs_l = rs;
+      rs_l.y = lsign * rs.y;
+      uint32_t ev, od;
+      float dmax = 0.0f;
+      if (noclamp)
+        act_chunk_fast_noclamp(v[c], rs_l, ev, od, dmax);
+      else
+        act_chunk_fast(v[c], rs_l, ev, od, dmax);
+      if (dmax >= rs.thr) act_chunk_exact(v[c], rs, lsign, ev, od);
+      const int64_t e0 = (int64_t)blk * 128 + jj[c] * 32 + qr * 8;
+      // (q - 8) & 15 == q ^ 8; elements in [K, KP) hold the zero-point's code.
+      if (e0 < d.KP)
+        *reinterpret_cast<uint32_t*>(a_lds + row * d.KB + e0 / 2) =
+            (ev | (od << 4)) ^ 0x88888888u;
+      if (blk == 0 && jj[c] == 0 && qr == 0) {
+        rsx[row] = rs.scale;
+        rzx[row] = (int32_t)rs.zf;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. dot products: per 64-byte block two v_mfma_i32_16x16x64_i8 (A row
+  // lane % 16 from LDS, zero past M; B from registers), as the skinny-M GEMM.
+  v4i acc = {0, 0, 0, 0};
+  const bool arow_live = r < d.M;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (i < per) {
+      const int64_t kb = (b0 + i) * 64;
+      const bool in = kb + off < d.KB;
+      uint4 av = make_uint4(0u, 0u, 0u, 0u);
+      if (arow_live && in) av = *reinterpret_cast<const uint4*>(a_lds + r * d.KB + kb + off);
+      uint4 bw = bv[i];
+      bw.x = in ? bw.x : 0u;
+      bw.y = in ? bw.y : 0u;
+      bw.z = in ? bw.z : 0u;
+      bw.w = in ? bw.w : 0u;
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(av.x, av.y), unpack8(bw.x, bw.y),
+                                                  acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(av.z, av.w), unpack8(bw.z, bw.w),
+                                                  acc, 0, 0, 0);
+    }
+  }
+  // D of a 16 x 16 tile: row (A) 4 * (lane / 16) + v, column (B) lane % 16.
+#pragma unroll
+  for (int t = 0; t < 4; ++t) part[wave][4 * grp + t][r] = acc[t] >> 8;
+  __syncthreads();
+  if (tid >= 256) return;
+  const int ml = tid >> 4, nl = tid & 15;
+  const int64_t m = ml, n = n0 + nl;
+  if (m >= d.M || n >= d.N) return;
+  int32_t rawv = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) rawv += part[w][ml][nl];
+  // Operation order of kernel/w4a4.cu:74-77.
+  const int32_t corrected = rawv + (8 - rzx[ml]) * d.sums[n];
+  float res = (float)corrected * rsx[ml];
+  res = res * d.sw[n];
+  if (BIAS) res = res + (float)static_cast<const OutT*>(d.bias)[n];
+  static_cast<OutT*>(d.out)[m * d.N + n] = to_out<OutT>(res);
+}
+
+}  // namespace
+
+// The limits the fused kernel accepts (see the file comment); callers check
+// them with linear_decode_fits and otherwise quantize and multiply separately.
+bool linear_decode_fits(int64_t M, int64_t K) {
+  const int64_t KP = ceil_to(K, 64), KB = KP / 2;
+  const int64_t nblk = (KP + 127) / 128;
+  return M >= 1 && M <= kWaves && K % 8 == 0 && M * nblk <= kMaxBlocks && M * KB <= kMaxABytes &&
+         (KB + 63) / 64 <= (int64_t)kWaves * kMaxBlocksPerWave;
+}
+
+int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, int rotate_block,
+                  const uint8_t* b, const float* sw, const int32_t* sums, const void* bias,
+                  int64_t N, bool out_fp32, void* out, hipStream_t stream) {
+  DecodeArgs d;
+  d.x = x;
+  d.M = M;
+  d.K = K;
+  d.KP = ceil_to(K, 64);
+  d.KB = d.KP / 2;
+  d.nblk = (int)((d.KP + 127) / 128);
+  d.clip = clip;
+  d.b = b;
+  d.brows = ceil_to(N, 8);
+  d.sw = sw;
+  d.sums = sums;
+  d.bias = bias;
+  d.N = N;
+  d.out = out;
+  const dim3 grid((unsigned)((N + 15) / 16)), block(kWaves * 64);
+  const bool rot = rotate_block != 0;
+  const int64_t per = ((d.KB + 63) / 64 + kWaves - 1) / kWaves;
+  // 16-lane blocks for up to two passes of 32 blocks, quads beyond.
+  const int64_t iters = (M * d.nblk + 31) / 32;
+#define DSCQ_DEC_I(T, O, R, B, P)                                                              \
+  if (iters <= 1)                                                                              \
+    hipLaunchKernelGGL((w4a4_decode_kernel<T, O, R, B, P, 1>), grid, block, 0, stream, d);    \
+  else if (iters <= 2)                                                                         \
+    hipLaunchKernelGGL((w4a4_decode_kernel<T, O, R, B, P, 2>), grid, block, 0, stream, d);    \
+  else                                                                                         \
+    hipLaunchKernelGGL((w4a4_decode_kernel<T, O, R, B, P, 0>), grid, block, 0, stream, d);
+#define DSCQ_DEC(T, O, R, B)                                                                   \
+  if (per <= 4) {                                                                              \
+    DSCQ_DEC_I(T, O, R, B, 4)                                                                  \
+  } else if (per <= 8) {                                                                       \
+    DSCQ_DEC_I(T, O, R, B, 8)                                                                  \
+  } else {                                                                                     \
+    DSCQ_DEC_I(T, O, R, B, 12)                                                                 \
+  }
+#define DSCQ_DEC_B(T, O, R) \
+  if (bias) { DSCQ_DEC(T, O, R, true); } else { DSCQ_DEC(T, O, R, false); }
+#define DSCQ_DEC_R(T, O) \
+  if (rot) { DSCQ_DEC_B(T, O, true) } else { DSCQ_DEC_B(T, O, false) }
+#define DSCQ_DEC_O(T) \
+  if (out_fp32) { DSCQ_DEC_R(T, float) } else { DSCQ_DEC_R(T, __half) }
+  if (dtype == DSCQ_F16) {
+    DSCQ_DEC_O(__half)
+  } else {
+    DSCQ_DEC_O(float)
+  }
+#undef DSCQ_DEC_O
+#undef DSCQ_DEC_R
+#undef DSCQ_DEC_B
+#undef DSCQ_DEC
+#undef DSCQ_DEC_I
+  return launch_status("w4a4_decode_kernel");
+}
+
+}  // namespace dscq

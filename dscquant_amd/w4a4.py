@@ -25,8 +25,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["quantize", "matmul", "pack_weight", "silu_mul_quantize", "padded",
-           "check_quantize_args", "check_matmul_args"]
+__all__ = ["quantize", "matmul", "pack_weight", "silu_mul_quantize", "linear_decode",
+           "linear_decode_supported", "padded", "check_quantize_args", "check_matmul_args"]
 
 
 def padded(v: int, m: int) -> int:
@@ -134,6 +134,45 @@ def matmul(a, b, sx, zx, sw, sums, bias, M: int, N: int, fused: bool = True,
                   1 if fused else 0, 1 if force_decode else 0, 1 if fp32 else 0,
                   out.data_ptr(), _lib.ptr(raw), _lib.stream(dev))
     return [out, raw]
+
+
+def linear_decode_supported(M: int, K: int) -> bool:
+    """Whether ``linear_decode`` takes an [M, K] input (a few tokens; see include/dscq.h)."""
+    return bool(_lib.lib().dscq_linear_decode_supported(int(M), int(K)))
+
+
+def linear_decode(x: torch.Tensor, clip: float, rotate_block: int, b, sw, sums, bias,
+                  N: int, fp32: bool = False) -> torch.Tensor:
+    """quantize(x, clip, True, rotate_block) followed by matmul(..., fused=True) in one
+    launch, for few tokens; bit-identical to the two calls.  ``b``, ``sw``, ``sums``,
+    ``bias`` as for ``matmul``.  Returns out [M, N] fp16 (fp32 if ``fp32``)."""
+    clip = float(clip)
+    check_quantize_args(x, clip, rotate_block)
+    M, K = x.shape
+    N = int(N)
+    KP = padded(K, 64)
+    for t in (b, sw, sums, bias):
+        _check_cuda(t)
+        if t.device != x.device:
+            raise RuntimeError("All buffers must be on the same device")
+    if not (b.dim() == 2 and b.dtype == torch.uint8 and b.size(1) * 2 == KP
+            and b.size(0) >= padded(N, 8) and N > 0):
+        raise RuntimeError("Invalid padded operand shapes")
+    if not (sw.dtype == torch.float32 and sums.dtype == torch.int32
+            and sw.numel() >= padded(N, 8) and sums.numel() >= padded(N, 8)):
+        raise RuntimeError("Invalid metadata dtypes")
+    dtype = torch.float32 if fp32 else torch.float16
+    if not (bias.dtype == dtype and (bias.numel() == 0 or bias.numel() == N)):
+        raise RuntimeError("Bias shape/dtype mismatch")
+    dev = x.device
+    _lib.require_gfx950(dev)
+    out = torch.empty((M, N), dtype=dtype, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("dscq_linear_decode", x.data_ptr(),
+                  _lib.F16 if x.dtype == torch.float16 else _lib.F32, M, K, clip, rotate_block,
+                  b.data_ptr(), sw.data_ptr(), sums.data_ptr(), _lib.ptr(bias), N,
+                  1 if fp32 else 0, out.data_ptr(), _lib.stream(dev))
+    return out
 
 
 def pack_weight(w: torch.Tensor, clip: float = 1.0, rotate_block: int = 0,

@@ -160,6 +160,30 @@ int dscq_unpack_int4(const uint8_t* packed, int64_t R, int64_t CB,
                      int64_t width, int8_t* codes, void* stream);
 
 /*
+ * Fused decode linear: the quantize and matmul steps of a W4A4 linear layer
+ * in one launch, for a few tokens.  Equal, bit for bit, to
+ *   dscq_quantize(x, x_dtype, M, K, clip, fused = 1, rotate_block, a, sx, zx)
+ *   dscq_matmul(a, b, sx, zx, sw, sums, bias, M, N, KP, fused = 1, ...)
+ * (kernel/w4a4.cu:164-225 called back to back, as QuantLinear's forward
+ * does, core/linear.py:48-52), without the intermediate buffers.  Each
+ * workgroup re-quantizes the M rows it needs while its weight stripe streams
+ * in, so the launch costs what the weight stream costs.
+ *   x      fp16 / fp32 [M, K], 16-byte aligned, K % 8 == 0.
+ *   b, sw, sums, bias, out_fp32, out  as dscq_matmul (b: [>= NP, KP/2]).
+ * Limits: dscq_linear_decode_supported(M, K) must hold (M <= 4 at K = 4096,
+ * M = 1 up to K = 12288); otherwise DSCQ_EINVAL, and the caller runs
+ * dscq_quantize + dscq_matmul.  No reference counterpart: it replaces the
+ * pair above on the decode path.
+ */
+int dscq_linear_decode(const void* x, int x_dtype, int64_t M, int64_t K, float clip,
+                       int rotate_block, const uint8_t* b, const float* sw,
+                       const int32_t* sums, const void* bias, int64_t N, int out_fp32,
+                       void* out, void* stream);
+
+/* 1 if dscq_linear_decode accepts an [M, K] input, else 0. */
+int dscq_linear_decode_supported(int64_t M, int64_t K);
+
+/*
  * 1 if the current HIP device is a gfx950 (MI355X-class) GPU the kernels
  * were built for, 0 if not, negative hipError_t if no device is usable.
  * Replaces the SM75-89 capability check of kernel/w4a4.cu:204-206.

@@ -97,6 +97,36 @@ def test_c_other_argument_checks():
                                         d, d, d, None, None)
 
 
+def test_c_linear_decode_limits_and_checks():
+    L = _lib.lib()
+    # One 128-element block per quad of a 512-lane workgroup: M * ceil(KP/128) <= 128.
+    assert L.dscq_linear_decode_supported(1, 4096) == 1
+    assert L.dscq_linear_decode_supported(4, 4096) == 1
+    assert L.dscq_linear_decode_supported(5, 4096) == 0
+    assert L.dscq_linear_decode_supported(2, 8192) == 1
+    assert L.dscq_linear_decode_supported(1, 11008) == 1
+    assert L.dscq_linear_decode_supported(2, 11008) == 0
+    assert L.dscq_linear_decode_supported(1, 16384) == 0   # weight stripe > 12 blocks/wave
+    assert L.dscq_linear_decode_supported(1, 4100) == 0    # K % 8
+    assert L.dscq_linear_decode_supported(0, 64) == 0
+    d = 16
+    # (x, dtype, M, K, clip, rotate, b, sw, sums, bias, N, fp32, out, stream)
+    assert "exceed" in _einval("dscq_linear_decode", d, 0, 5, 4096, 1.0, 0, d, d, d, None, 8,
+                               0, d, None)
+    assert _einval("dscq_linear_decode", d, 3, 1, 64, 1.0, 0, d, d, d, None, 8, 0, d,
+                   None) == "Only FP16 and FP32 inputs are supported"
+    assert _einval("dscq_linear_decode", d, 0, 1, 64, 1.0, 0, d, d, d, None, 0, 0, d,
+                   None) == "Invalid dimensions"
+    assert "clip" in _einval("dscq_linear_decode", d, 0, 1, 64, 0.2, 0, d, d, d, None, 8, 0, d,
+                             None)
+    assert "multiple of 128" in _einval("dscq_linear_decode", d, 0, 1, 192, 1.0, 128, d, d, d,
+                                        None, 8, 0, d, None)
+    assert "null" in _einval("dscq_linear_decode", d, 0, 1, 64, 1.0, 0, None, d, d, None, 8, 0,
+                             d, None)
+    assert "aligned" in _einval("dscq_linear_decode", 8, 0, 1, 64, 1.0, 0, d, d, d, None, 8, 0,
+                                d, None)
+
+
 # ------------------------------------------------------- Python-side messages
 
 def test_quantize_messages_match_reference():

@@ -72,6 +72,9 @@ def parse():
     p.add_argument("--kernels-only", action="store_true",
                    help="launch only the quantize kernel, the GEMM and a 16 MiB device copy "
                         "(--kernel-iters each), for rocprofv3 --pmc passes")
+    p.add_argument("--vendor-int8", action="store_true",
+                   help="context only: time the vendor library's int8 GEMM (torch._int_mm, "
+                        "hipBLASLt) and fp16 matmul at the prefill and 70B shapes")
     p.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                    help="turn two rocprofv3 --pmc counter_collection.csv files of a "
                         "--kernels-only run (FETCH_SIZE, WRITE_SIZE) into HBM bytes per launch, "
@@ -119,7 +122,9 @@ COPY_BYTES = 16 << 20
 
 def kernel_class(name):
     if "row_quant" in name:
-        return "quantize"
+        # template arguments <T, ROT, MODE, ...>: MODE 1 is the weight pre-pack
+        args = name.split("row_quant_kernel<", 1)[-1].split(",")
+        return "pack" if len(args) > 2 and args[2].strip() == "1" else "quantize"
     if "w4a4_gemm" in name or "w4a4_gemv" in name:
         return "gemm"
     if "w4a4_decode" in name:
@@ -142,6 +147,8 @@ def traffic_summary(fetch_csv, write_csv):
                 continue
             acc.setdefault(cls, []).append(float(row["Counter_Value"]) * 1024.0)
         for cls, v in acc.items():
+            if cls == "copy":  # the 16 MiB calibration copies, not small setup copies
+                v = [x for x in v if x >= 0.5 * max(v)]
             means.setdefault(cls, {})[counter] = sum(v) / len(v)
     f_fetch = COPY_BYTES / means["copy"]["FETCH_SIZE"]
     f_write = COPY_BYTES / means["copy"]["WRITE_SIZE"]
@@ -198,6 +205,8 @@ def main():
     if args.traffic:
         print(json.dumps(traffic_summary(*args.traffic), indent=1))
         return
+    if args.vendor_int8:
+        return vendor_int8()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(this build runs the path on a single MI355X)", file=sys.stderr)
@@ -409,6 +418,37 @@ def run_graph_steps(args, torch, dev, step):
     run(timed)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / args.steps
+
+
+def vendor_int8():
+    """The platform library's dense int8 GEMM (hipBLASLt through torch._int_mm: int8
+    operands, int32 result, no int4 unpacking, no epilogue) and fp16 matmul, as a
+    reference point for the W4A4 kernel.  B is K-contiguous (the layout this build's
+    GEMM reads).  Not part of the default run."""
+    import torch
+    dev = torch.device("cuda:0")
+    res = {}
+    for M, N, K in ((2048, 4096, 4096), (4096, 8192, 8192)):
+        a = torch.randint(-8, 8, (M, K), dtype=torch.int8, device=dev)
+        b = torch.randint(-8, 8, (N, K), dtype=torch.int8, device=dev).t()  # [K, N], K-contiguous
+        ah, bh = a.half(), b.half()
+        for name, fn in (("int8 torch._int_mm", lambda: torch._int_mm(a, b)),
+                         ("fp16 matmul", lambda: ah @ bh)):
+            fn()
+            torch.cuda.synchronize()
+            times = []
+            for _ in range(5):
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                for _ in range(50):
+                    fn()
+                e.record()
+                e.synchronize()
+                times.append(s.elapsed_time(e) / 50 * 1e3)
+            us = sorted(times)[2]
+            res[f"{name} {M}x{N}x{K}"] = {"us": round(us, 2),
+                                           "TOPS": round(2.0 * M * N * K / us / 1e6, 1)}
+    print(json.dumps({"vendor_gemm": res}))
 
 
 def main_decode(args, torch, _lib, w4a4):

@@ -7,26 +7,33 @@
 // Both operands are row-major with K contiguous (TN): a [>= MP, KP/2],
 // b [>= NP, KP/2].
 //
-// CDNA4 has no int4 MFMA.  A packed dword w holds 8 nibbles; the two dwords
-//   lo = (w << 4) & 0xF0F0F0F0   (even k, each byte = 16 * nibble value)
-//   hi =  w       & 0xF0F0F0F0   (odd k)
-// are 8 int8 values scaled by 16 with the sign in the byte's top bit, so one
-// shift and two ANDs unpack 8 k-values.  A and B go through the same k
-// permutation, so the dot product is unchanged and carries a factor 256,
-// removed exactly by an arithmetic >> 8 (the accumulator is a multiple of
-// 256).  |partial sums| <= 256 * 64 * K stays below 2^31 for K <= 65536;
-// longer rows drain the accumulator into an unscaled total every 65536 k.
+// CDNA4 has no int4 MFMA: both operands are unpacked from nibbles to int8 in
+// registers (mma_int4.h), so every dot product carries a factor 256, removed
+// exactly by an arithmetic >> 8.  |partial sums| <= 256 * 64 * K stays below
+// 2^31 for K <= 65536; longer rows drain the accumulator into an unscaled
+// total every 65536 k.
 //
-// Tiling.  A workgroup owns a BM x BN output tile; WM x WN waves each own a
-// (BM/WM) x (BN/WN) sub-tile made of 32 x 32 v_mfma_i32_32x32x32_i8 tiles.
-// The K loop walks 128-nibble (64-byte) slices: each slice of A and B is
-// staged in LDS as four 16-byte "planes" (k-bytes 0-15, 16-31, ...), one per
-// MFMA k-step, laid out [plane][row][16 B] so a fragment read -- lane l takes
-// row l % 32, bytes 8 * (l / 32) .. +7 -- is one conflict-free ds_read_b64.
-// Planes are padded by 64 bytes so the 16-byte writes of four consecutive
-// lanes (one 64-byte global segment of a row) land in distinct banks.  Two
-// LDS stages double-buffer the slices: global loads for slice k+1 are in
-// flight while slice k feeds the matrix cores; one barrier per slice.
+// Kernels (dispatch in gemm_typed):
+//   w4a4_gemm_pipe_kernel  the main kernel (M >= 64, N % 8 == 0): 256-nibble
+//                          slices, swizzled LDS rows, two slices of global
+//                          loads in flight, one barrier per slice (its own
+//                          comment below);
+//   w4a4_gemv_kernel       M <= 16 or force_decode: weights streamed once,
+//                          K split over the waves of a workgroup;
+//   w4a4_gemm_kernel       everything else (16 < M < 64, N % 8 != 0, output not
+//                          16-byte aligned, KP > 65536): a simpler tiled kernel.
+//
+// w4a4_gemm_kernel tiling.  A workgroup owns a BM x BN output tile; WM x WN
+// waves each own a (BM/WM) x (BN/WN) sub-tile made of 32 x 32
+// v_mfma_i32_32x32x32_i8 tiles.  The K loop walks 128-nibble (64-byte) slices:
+// each slice of A and B is staged in LDS as four 16-byte "planes" (k-bytes
+// 0-15, 16-31, ...), one per MFMA k-step, laid out [plane][row][16 B] so a
+// fragment read -- lane l takes row l % 32, bytes 8 * (l / 32) .. +7 -- is one
+// conflict-free ds_read_b64.  Planes are padded by 64 bytes so the 16-byte
+// writes of four consecutive lanes (one 64-byte global segment of a row) land
+// in distinct banks.  Two LDS stages double-buffer the slices: global loads
+// for slice k+1 are in flight while slice k feeds the matrix cores; one
+// barrier per slice.
 
 #include <cstdlib>
 #include <cstring>

@@ -430,28 +430,34 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
 
   // st_next holds slice s + 1 (loaded during slice s - 1); st_free held
   // slice s, already in LDS, and now receives slice s + 2.
-  auto slice = [&](int s, uint4 (&st_next)[LOADS], uint4 (&st_free)[LOADS]) {
+  // FIRST (slice 0 only): the writes of slice 1 move to steps 2-4, so the
+  // loop starts as soon as slice 0 has arrived instead of waiting for both.
+  auto slice = [&](int s, uint4 (&st_next)[LOADS], uint4 (&st_free)[LOADS], auto first) {
+    constexpr bool FIRST = decltype(first)::value;
     const int cbuf = s & 1, nbuf = cbuf ^ 1;
     mfma_step(U0);
     unpack_step(U1, 1);
     gload(st_free, s + 2);
-    lstore(st_next, nbuf, C0{}, C1{});
+    if (!FIRST) lstore(st_next, nbuf, C0{}, C1{});
     interleave();
     mfma_step(U1);
     unpack_step(U0, 2);
     lread(cbuf, 2);
-    lstore(st_next, nbuf, C1{}, C2{});
+    if (!FIRST) lstore(st_next, nbuf, C1{}, C2{});
     interleave();
     mfma_step(U0);
     unpack_step(U1, 3);
-    lstore(st_next, nbuf, C2{}, C3{});
+    if (FIRST) lstore(st_next, nbuf, C0{}, C1{});
+    else lstore(st_next, nbuf, C2{}, C3{});
     interleave();
     mfma_step(U1);
     unpack_step(U0, 4);
     lread(cbuf, 3);
+    if (FIRST) lstore(st_next, nbuf, C1{}, C2{});
     interleave();
     mfma_step(U0);
     unpack_step(U1, 5);
+    if (FIRST) lstore(st_next, nbuf, C2{}, C3{});
     interleave();
     // Slice s + 1 is complete in LDS once every wave passes here; its first
     // fragments (P[0], P[1]: free since step 2) are read over the next two
@@ -470,12 +476,13 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     interleave();
   };
   // Slice s + 1 sits in G1 when s is even, in G0 when s is odd.
-  int s = 0;
+  slice(0, G1, G0, std::true_type{});
+  int s = 1;
   for (; s + 1 < nslices; s += 2) {
-    slice(s, G1, G0);
-    slice(s + 1, G0, G1);
+    slice(s, G0, G1, std::false_type{});
+    slice(s + 1, G1, G0, std::false_type{});
   }
-  if (s < nslices) slice(s, G1, G0);
+  if (s < nslices) slice(s, G0, G1, std::false_type{});
 
   // ---- epilogue.  The MFMAs took B as their first operand, so acc[i][j] is
   // the transposed 32 x 32 tile: output row m, column n sits in lane

@@ -575,13 +575,39 @@ int launch_pipe_cfg(GemmArgs g, hipStream_t stream) {
   return launch_status("w4a4_gemm_pipe_kernel");
 }
 
-// The largest tile that still gives every CU a workgroup: 256 x 128 (two
-// waves per SIMD), else 128 x 128 or 64 x 128 (two workgroups per CU).
+// Compute units of the current device (cached per device; 256 on MI355X).
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Tile choice.  256 x 128 tiles (one workgroup per CU, two waves per SIMD)
+// move the least data per MFMA and win whenever their rounds of one tile per
+// CU are well filled: a whole number of rounds, a last round more than 60%
+// full, or a single round over at least 60% of the CUs (measured: M=512,
+// N=11008 runs 13% faster on 172 CUs with 256 x 128 than on all of them with
+// 128 x 128).  Otherwise 128 x 128 or 64 x 128 tiles, two workgroups per CU,
+// spread the work over every CU (M=512, N=22016: 1.34 rounds of 256 x 128 and
+// 128 x 128 measure the same; M=512, N=4096, K=11008: 64 x 128 is 22% faster
+// than 128 x 128 and 37% faster than a quarter-full round of 256 x 128).
 template <typename OutT>
 int launch_pipe(GemmArgs g, hipStream_t stream) {
+  const int64_t cus = cu_count();
   const int64_t tn = (g.N + 127) / 128;
-  if (((g.M + 255) / 256) * tn >= 256) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
-  if (((g.M + 127) / 128) * tn >= 256) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
+  const int64_t t256 = ((g.M + 255) / 256) * tn;
+  const int64_t last = t256 % cus;
+  if ((t256 >= cus && (last == 0 || 10 * last > 6 * cus)) || (t256 < cus && 10 * t256 >= 6 * cus))
+    return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
+  if (((g.M + 127) / 128) * tn >= cus) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
   return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2>(g, stream);
 }
 

@@ -43,18 +43,25 @@ MALL_BYTES = 256 << 20
 WORKLOADS = {
     # name: (M, N, K, rotate_block)
     "prefill": (2048, 4096, 4096, 128),
-    "decode16": (16, 4096, 4096, 128),
     "mlp_up": (512, 11008, 4096, 128),
     "mlp_down": (512, 4096, 11008, 128),
     "70b_qo": (4096, 8192, 8192, 128),
+    "70b_up": (4096, 28672, 8192, 128),
+    "70b_down": (4096, 8192, 28672, 128),
     # SiLU-gated MLP block (Llama-7B shapes): x[M,K] -> gate|up GEMM [M, 2N] ->
     # silu*up + rotate + quantize -> down GEMM [M, K]
     "mlp": (512, 11008, 4096, 128),
-    # decode: one fused launch (dscq_linear_decode) per step; the packed weights
+    # decode: one fused launch (dscq_linear_decode) per step where it applies
+    # (M * K / 128 <= 128), else quantize + the skinny-M GEMM; the packed weights
     # cycle through more than the Infinity Cache, so they stream from HBM
     "decode1": (1, 4096, 4096, 128),
     "decode4": (4, 4096, 4096, 128),
+    "decode8": (8, 4096, 4096, 128),
+    "decode16": (16, 4096, 4096, 128),
     "decode1_up": (1, 11008, 4096, 128),
+    "decode4_up": (4, 11008, 4096, 128),
+    "decode8_up": (8, 11008, 4096, 128),
+    "decode16_up": (16, 11008, 4096, 128),
 }
 
 
@@ -174,29 +181,51 @@ def load_traffic(workload):
     return json.loads(m.group(1)) if m else None
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(M, N, K, budget_s):
-    """The reference's CPU fake-quant forward on the same workload, median time."""
+    """The reference's CPU fake-quant forward on the same workload, median time:
+    as the reference runs it (weight re-quantized on every call) and with the
+    fake-quantized weight cached, each on half of the time budget."""
     import torch
     from oracle import fakequant
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
     x, w = synthetic(M, N, K)
-    fakequant.forward(x, w, None)  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 30):
-        t0 = time.perf_counter()
-        fakequant.forward(x, w, None)
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
+
+    def median_time(fn, budget):
+        fn()  # warm-up
+        times = []
+        t_end = time.perf_counter() + budget
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 30):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return sorted(times)[len(times) // 2], len(times)
+
+    med, n = median_time(lambda: fakequant.forward(x, w, None), budget_s / 2)
+    w_hat = fakequant.quantize_weight(w, 4)
+    med_c, n_c = median_time(lambda: fakequant.forward(x, w, None, w_hat=w_hat), budget_s / 2)
+    ops = 2.0 * M * N * K
     return {
-        "value": round(2.0 * M * N * K / med / 1e12, 4),
+        "value": round(ops / med / 1e12, 4),
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
         "sample": (f"torch-CPU fake-quant QuantLinear.forward (core/linear.py:48-52), "
                    f"weights re-quantized per call, M={M} N={N} K={K} fp16, "
-                   f"median of {len(times)} runs ({med * 1e3:.1f} ms/run)"),
+                   f"median of {n} runs ({med * 1e3:.1f} ms/run) on {threads} threads of "
+                   f"{cpu_model()}"),
+        "weights_cached": {"value": round(ops / med_c / 1e12, 4), "unit": "TOPS",
+                           "ms_per_run": round(med_c * 1e3, 2), "runs": n_c},
     }
 
 
@@ -217,7 +246,7 @@ def main():
 
     if args.workload == "mlp":
         return main_mlp(args, torch, _lib, w4a4)
-    if args.workload.startswith("decode") and args.workload != "decode16":
+    if args.workload.startswith("decode"):
         return main_decode(args, torch, _lib, w4a4)
 
     dev = torch.device("cuda:0")
@@ -452,16 +481,17 @@ def vendor_int8():
 
 
 def main_decode(args, torch, _lib, w4a4):
-    """Decode-shaped W4A4 linear (a few tokens): the fused quantize + skinny
-    product kernel, one launch per step, against HBM bandwidth; the two-launch
-    path (quantize, then the skinny-M GEMM) is timed beside it."""
+    """Decode-shaped W4A4 linear (a few tokens), against HBM bandwidth.  Where
+    the fused kernel applies (dscq_linear_decode: quantize + skinny product in
+    one launch) a step is that launch; otherwise a step is quantize + the
+    skinny-M GEMM.  The two-launch path is timed beside the fused one."""
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     _lib.require_gfx950(dev)
     M, N, K, rot = WORKLOADS[args.workload]
     MP, KP = (M + 7) // 8 * 8, (K + 63) // 64 * 64
     L = _lib.lib()
-    assert L.dscq_linear_decode_supported(M, K)
+    fused_ok = bool(L.dscq_linear_decode_supported(M, K))
     x, w = synthetic(M, N, K)
     wbytes = N * KP // 2
     nw = max(2, math.ceil(2 * MALL_BYTES / wbytes))
@@ -482,39 +512,66 @@ def main_decode(args, torch, _lib, w4a4):
                                 sw.data_ptr(), sums.data_ptr(), None, N, 0, out.data_ptr(),
                                 _lib.stream(dev)))
 
-    def two_launch(i):
-        pw, sw, sums = packs[i % nw]
+    def quantize(i):
         ok(L.dscq_quantize(xs[i % 8].data_ptr(), _lib.F16, M, K, 1.0, 1, rot, pa.data_ptr(),
                            sx.data_ptr(), zx.data_ptr(), None, _lib.stream(dev)))
+
+    def gemv(i):
+        pw, sw, sums = packs[i % nw]
         ok(L.dscq_matmul(pa.data_ptr(), pw.data_ptr(), sx.data_ptr(), zx.data_ptr(),
                          sw.data_ptr(), sums.data_ptr(), None, M, N, KP, 1, 0, 0,
                          out.data_ptr(), None, _lib.stream(dev)))
 
+    def two_launch(i):
+        quantize(i)
+        gemv(i)
+
+    step = fused if fused_ok else two_launch
     if args.kernels_only:
         srcs = [torch.ones(COPY_BYTES // 2, dtype=torch.float16, device=dev)
                 for _ in range(2 * MALL_BYTES // COPY_BYTES + 2)]
         dst = torch.empty_like(srcs[0])
         for i in range(args.kernel_iters):
-            fused(i)
+            step(i)
         for i in range(args.kernel_iters):
             dst.copy_(srcs[i % len(srcs)])
         torch.cuda.synchronize()
-        print(f"kernels-only: {args.kernel_iters} launches each of the fused decode kernel, "
+        print(f"kernels-only: {args.kernel_iters} steps ("
+              f"{'fused decode kernel' if fused_ok else 'quantize + skinny-M GEMM'}), "
               f"{COPY_BYTES >> 20} MiB copy", flush=True)
         return
 
-    t_fused = time_kernel(fused, args.kernel_iters, torch, dev)
     t_two = time_kernel(two_launch, args.kernel_iters, torch, dev)
-    t_step = run_graph_steps(args, torch, dev, fused)
+    t_quant = time_kernel(quantize, args.kernel_iters, torch, dev)
+    quantize(0)
+    t_gemv = time_kernel(gemv, args.kernel_iters, torch, dev)
+    t_fused = time_kernel(fused, args.kernel_iters, torch, dev) if fused_ok else None
+    t_step = run_graph_steps(args, torch, dev, step)
     ops = 2.0 * M * N * K
-    # weights + x (fp16) + sw, sums + out (fp16)
-    dbytes = wbytes + 2 * M * K + 8 * N + 2 * M * N
-    gbs = dbytes / t_fused / 1e9
-    traffic = load_traffic(args.workload)
-    line = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(gbs / PEAK_HBM_GBS, 4), "kernel": "w4a4_decode_kernel",
-            "avg_us": round(t_fused * 1e6, 3), "bytes_per_launch": dbytes,
-            "traffic": (traffic["decode"]["traffic"] if traffic and "decode" in traffic else None)}
+    traffic = load_traffic(args.workload) or {}
+
+    def hbm_line(kernel, dbytes, t, cls):
+        gbs = dbytes / t / 1e9
+        return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(gbs / PEAK_HBM_GBS, 4), "kernel": kernel,
+                "avg_us": round(t * 1e6, 3), "bytes_per_launch": dbytes,
+                "traffic": traffic[cls]["traffic"] if cls in traffic else None}
+
+    # skinny GEMM: packed weights + packed activations + sw, sums, sx, zx + out (fp16)
+    gemv_line = hbm_line("w4a4_gemv_kernel", wbytes + M * KP // 2 + 8 * N + 8 * M + 2 * M * N,
+                         t_gemv, "gemm")
+    kernels = {"quantize": {"avg_us": round(t_quant * 1e6, 3)}, "gemv": gemv_line,
+               "quantize_then_matmul": {"avg_us": round(t_two * 1e6, 3),
+                                        "note": "two launches"}}
+    if fused_ok:
+        # weights + x (fp16) + sw, sums + out (fp16)
+        line = hbm_line("w4a4_decode_kernel", wbytes + 2 * M * K + 8 * N + 2 * M * N, t_fused,
+                        "decode")
+        kernels = {"decode_fused": line, **kernels}
+        how = "fused quantize + skinny product (one launch)"
+    else:
+        line = gemv_line
+        how = "quantize + skinny-M GEMM (M * K / 128 > 128: no fused kernel)"
     cpu = None if args.no_cpu else cpu_baseline(M, N, K, args.cpu_seconds)
     result = {
         "metric": METRIC,
@@ -530,13 +587,10 @@ def main_decode(args, torch, _lib, w4a4):
         "dtype": "int4xint4->int32 (int8 MFMA), fp16 in/out",
         "data": "synthetic: X~N(0,1) fp16 with 1% outlier channels x50, W~N(0,0.02), seeded",
         "config": {"workload": f"{args.workload}: W4A4 linear M={M} K={K} N={N}, rotate_block="
-                               f"{rot}, fused quantize + skinny product, {nw} weight sets "
-                               f"cycled (HBM-resident)",
+                               f"{rot}, {how}, {nw} weight sets cycled (HBM-resident)",
                    "M": M, "N": N, "K": K, "rotate_block": rot, "weight_sets": nw},
         "roofline": line,
-        "kernels": {"decode_fused": line,
-                    "quantize_then_matmul": {"avg_us": round(t_two * 1e6, 3),
-                                             "note": "two launches, same result"}},
+        "kernels": kernels,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))

@@ -132,6 +132,12 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
     const bool in = i < per && kb + off < d.KB;
     bv[i] = *reinterpret_cast<const uint4*>(brow + (in ? kb + off : d.KB - 16));
   }
+  // Epilogue operands of column n0 + tid % 16, fetched now by every thread
+  // (index clamped; threads < 256 use them) instead of after the dot products.
+  const int64_t nc = min(n0 + (tid & 15), d.N - 1);
+  const float e_sw = d.sw[nc];
+  const int32_t e_sum = d.sums[nc];
+  const float e_b = BIAS ? (float)static_cast<const OutT*>(d.bias)[nc] : 0.0f;
   // Keep every load above the arithmetic (the scheduler would otherwise sink
   // the weight loads below the transform to save registers).
   __builtin_amdgcn_sched_barrier(0);
@@ -298,10 +304,10 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) rawv += part[w][ml][nl];
   // Operation order of kernel/w4a4.cu:74-77.
-  const int32_t corrected = rawv + (8 - rzx[ml]) * d.sums[n];
+  const int32_t corrected = rawv + (8 - rzx[ml]) * e_sum;
   float res = (float)corrected * rsx[ml];
-  res = res * d.sw[n];
-  if (BIAS) res = res + (float)static_cast<const OutT*>(d.bias)[n];
+  res = res * e_sw;
+  if (BIAS) res = res + e_b;
   static_cast<OutT*>(d.out)[m * d.N + n] = to_out<OutT>(res);
 }
 

@@ -648,6 +648,15 @@ __global__ __launch_bounds__(512) void w4a4_gemv_kernel(GemmArgs g) {
   const uint8_t* brow = g.b + min(n0 + r, g.brows - 1) * KB;
   const int64_t off = grp * 16;
 
+  // Epilogue operands of output (m0 + tid / 16 % 16, n0 + tid % 16), fetched
+  // up front by every thread (indices clamped; only threads < 256 use them) so
+  // that the epilogue does not wait for a second trip to memory.
+  const int ml = (tid >> 4) & 15, nl = tid & 15;
+  const int64_t mc = min(m0 + ml, g.arows - 1), nc = min(n0 + nl, g.brows - 1);
+  const float e_sx = g.sx[mc], e_sw = g.sw[nc];
+  const int32_t e_z = 8 - g.zx[mc], e_sum = g.sums[nc];
+  const float e_b = BIAS ? (float)static_cast<const OutT*>(g.bias)[min(n0 + nl, g.N - 1)] : 0.0f;
+
   v4i acc = {0, 0, 0, 0};
   int32_t tot[4] = {0, 0, 0, 0};
   auto piece = [&](const uint8_t* row, int64_t kb) {
@@ -693,17 +702,16 @@ __global__ __launch_bounds__(512) void w4a4_gemv_kernel(GemmArgs g) {
   for (int v = 0; v < 4; ++v) part[wave][4 * grp + v][r] = tot[v] + (acc[v] >> 8);
   __syncthreads();
   if (tid >= 256) return;
-  const int ml = tid >> 4, nl = tid & 15;
   int32_t raw = 0;
 #pragma unroll
   for (int w = 0; w < WAVES; ++w) raw += part[w][ml][nl];
   const int64_t m = m0 + ml, n = n0 + nl;
   if (m >= g.M || n >= g.N) return;
   // Operation order of kernel/w4a4.cu:74-77.
-  const int32_t corrected = raw + (8 - g.zx[m]) * g.sums[n];
-  float res = (float)corrected * g.sx[m];
-  res = res * g.sw[n];
-  if (BIAS) res = res + (float)static_cast<const OutT*>(g.bias)[n];
+  const int32_t corrected = raw + e_z * e_sum;
+  float res = (float)corrected * e_sx;
+  res = res * e_sw;
+  if (BIAS) res = res + e_b;
   static_cast<OutT*>(g.out)[m * g.N + n] = to_out<OutT>(res);
   if (g.raw) g.raw[m * g.N + n] = raw;
 }

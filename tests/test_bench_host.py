@@ -1,0 +1,106 @@
+"""Host-side logic of bench.py, on the CPU: kernel classification of profiler
+names, the HBM-traffic calibration arithmetic, the traffic blocks committed
+under profiles/, and the single-GPU contract (--gpus N > 1 exits with a message).
+"""
+import csv
+import json
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+
+@pytest.mark.parametrize("name,cls", [
+    ("void dscq::(anonymous namespace)::row_quant_kernel<__half, true, 0, 2, 1, true, false>"
+     "(dscq::(anonymous namespace)::RowArgs)", "quantize"),
+    ("void dscq::(anonymous namespace)::row_quant_kernel<__half, true, 1, 2, 1, false, false>"
+     "(dscq::(anonymous namespace)::RowArgs)", "pack"),
+    ("void dscq::(anonymous namespace)::w4a4_gemm_pipe_kernel<__half, 256, 128, 4, 2, 1, false, "
+     "false>(dscq::(anonymous namespace)::GemmArgs)", "gemm"),
+    ("void dscq::(anonymous namespace)::w4a4_gemv_kernel<__half, false>(GemmArgs)", "gemm"),
+    ("void dscq::(anonymous namespace)::w4a4_decode_kernel<__half, __half, true, false, 4, 1>"
+     "(DecodeArgs)", "decode"),
+    ("__amd_rocclr_copyBuffer", "copy"),
+    ("void at::native::roll_cuda_kernel<c10::Half>(c10::Half const*)", None),
+])
+def test_kernel_class(name, cls):
+    assert bench.kernel_class(name) == cls
+
+
+def _counter_csv(path, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for r in rows:
+            w.writerow(r)
+
+
+def test_traffic_summary_scales_by_the_copy(tmp_path):
+    """FETCH_SIZE reads half of what a 16 MiB copy moves (factor 2), WRITE_SIZE all of it;
+    small setup copies are left out of the calibration; the weight pack is not a class."""
+    mib = 1 << 20
+    copy = "__amd_rocclr_copyBuffer"
+    quant = "row_quant_kernel<__half, true, 0, 2, 1, true, false>"
+    pack = "row_quant_kernel<__half, true, 1, 2, 1, false, false>"
+    gemm = "w4a4_gemm_pipe_kernel<__half, 256, 128, 4, 2, 1, false, false>"
+    fetch = [
+        {"Kernel_Name": copy, "Counter_Name": "FETCH_SIZE", "Counter_Value": 8 * 1024},   # KiB
+        {"Kernel_Name": copy, "Counter_Name": "FETCH_SIZE", "Counter_Value": 8 * 1024},
+        {"Kernel_Name": copy, "Counter_Name": "FETCH_SIZE", "Counter_Value": 4},          # setup copy
+        {"Kernel_Name": quant, "Counter_Name": "FETCH_SIZE", "Counter_Value": 8 * 1024},
+        {"Kernel_Name": quant, "Counter_Name": "FETCH_SIZE", "Counter_Value": 9 * 1024},
+        {"Kernel_Name": pack, "Counter_Name": "FETCH_SIZE", "Counter_Value": 1e6},
+        {"Kernel_Name": gemm, "Counter_Name": "FETCH_SIZE", "Counter_Value": 20 * 1024},
+    ]
+    write = [
+        {"Kernel_Name": copy, "Counter_Name": "WRITE_SIZE", "Counter_Value": 16 * 1024},
+        {"Kernel_Name": quant, "Counter_Name": "WRITE_SIZE", "Counter_Value": 4 * 1024},
+        {"Kernel_Name": gemm, "Counter_Name": "WRITE_SIZE", "Counter_Value": 16 * 1024},
+    ]
+    fp, wp = tmp_path / "f.csv", tmp_path / "w.csv"
+    _counter_csv(fp, fetch)
+    _counter_csv(wp, write)
+    t = bench.traffic_summary(str(fp), str(wp))
+    assert t["calibration"]["fetch_factor"] == 2.0 and t["calibration"]["write_factor"] == 1.0
+    assert t["quantize"]["fetch_bytes"] == 17 * mib  # mean 8.5 MiB read by the counter, x2
+    assert t["quantize"]["write_bytes"] == 4 * mib
+    assert t["gemm"]["traffic"] == 40 * mib + 16 * mib
+    assert "pack" not in t and "decode" not in t
+
+
+@pytest.mark.parametrize("workload,classes", [
+    ("prefill", ("quantize", "gemm")),
+    ("decode1", ("decode",)),
+    ("decode16", ("quantize", "gemm")),
+])
+def test_committed_traffic_blocks(workload, classes):
+    """The blocks bench.py reads for roofline.traffic parse and are self-consistent."""
+    t = bench.load_traffic(workload)
+    assert t is not None
+    cal = t["calibration"]
+    assert cal["copy_bytes_each_way"] == bench.COPY_BYTES
+    assert abs(cal["fetch_factor"] - cal["copy_bytes_each_way"] / cal["fetch_counter_bytes"]) < 1e-3
+    for c in classes:
+        assert t[c]["traffic"] == t[c]["fetch_bytes"] + t[c]["write_bytes"]
+    if workload == "prefill":
+        M, N, K, _ = bench.WORKLOADS["prefill"]
+        # the GEMM writes exactly its fp16 output; the quantize kernel its packed codes + metadata
+        assert abs(t["gemm"]["write_bytes"] - 2 * M * N) < 1024
+        assert abs(t["quantize"]["write_bytes"] - (M * K // 2 + 8 * M)) < 64 * 1024
+
+
+def test_workloads_are_well_formed():
+    for name, (M, N, K, rot) in bench.WORKLOADS.items():
+        assert M > 0 and N % 8 == 0 and K % 128 == 0 and rot in (0, 128), name
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr or "single" in r.stderr

@@ -1,0 +1,88 @@
+"""The product path captured in a HIP graph (torch.cuda.CUDAGraph), as bench.py
+times it: every replay must read the current contents of its input buffers and
+give, bit for bit, what eager calls give on the same data.  Each replay is
+followed by eager work on the same stream and a synchronisation, and the inputs
+change between replays.  Covered: rotate+quantize+pack -> pipelined GEMM
+(prefill shape class), quantize -> skinny-M GEMM (16 tokens), the fused decode
+kernel, and the SiLU-gated requantization.
+"""
+import numpy as np
+import pytest
+import torch
+
+from dscquant_amd import w4a4
+from tests.conftest import activations, weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _capture(fn, static_in):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(static_in)  # warm the captured path outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn(static_in)
+    return g, out
+
+
+def _replay_and_compare(fn, inputs):
+    static_in = inputs[0].clone()
+    g, static_out = _capture(fn, static_in)
+    for rep, x in enumerate(inputs + inputs[::-1]):
+        static_in.copy_(x)
+        g.replay()
+        eager = fn(x)
+        torch.cuda.synchronize()
+        outs = static_out if isinstance(static_out, (list, tuple)) else [static_out]
+        refs = eager if isinstance(eager, (list, tuple)) else [eager]
+        for o, r in zip(outs, refs):
+            assert torch.equal(o, r), f"replay {rep} differs from eager"
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 4096, 1024), (16, 4096, 4096)])
+def test_quantize_matmul_graph(gpu, M, K, N):
+    print(f"graph quantize+matmul M{M} K{K} N{N}", flush=True)
+    pw, sw, sums = w4a4.pack_weight(torch.from_numpy(weights(N, K, seed=9)).to(gpu), 1.0, 128)
+    bias = torch.empty(0, dtype=torch.float16, device=gpu)
+
+    def run(x):
+        pa, sx, zx = w4a4.quantize(x, 1.0, True, 128)
+        out, _ = w4a4.matmul(pa, pw, sx, zx, sw, sums, bias, M, N)
+        return [out, pa, sx, zx]
+
+    xs = [torch.from_numpy(activations(M, K, seed=s).astype(np.float16)).to(gpu)
+          for s in (1, 2, 3)]
+    _replay_and_compare(run, xs)
+
+
+def test_linear_decode_graph(gpu):
+    M, K, N = 2, 4096, 4096
+    print(f"graph linear_decode M{M} K{K} N{N}", flush=True)
+    assert w4a4.linear_decode_supported(M, K)
+    pw, sw, sums = w4a4.pack_weight(torch.from_numpy(weights(N, K, seed=5)).to(gpu), 1.0, 128)
+    bias = torch.from_numpy((np.random.default_rng(0).standard_normal(N) * 0.1)
+                            .astype(np.float16)).to(gpu)
+
+    def run(x):
+        return w4a4.linear_decode(x, 1.0, 128, pw, sw, sums, bias, N)
+
+    xs = [torch.from_numpy(activations(M, K, seed=s).astype(np.float16)).to(gpu)
+          for s in (4, 5, 6)]
+    _replay_and_compare(run, xs)
+
+
+def test_silu_mul_quantize_graph(gpu):
+    M, N = 64, 1024
+    print(f"graph silu_mul_quantize M{M} N{N}", flush=True)
+
+    def run(gu):
+        return w4a4.silu_mul_quantize(gu, 1.0, 128, return_h=True)
+
+    rng = np.random.default_rng(7)
+    xs = [torch.from_numpy((rng.standard_normal((M, 2 * N)) * 2).astype(np.float16)).to(gpu)
+          for _ in range(3)]
+    _replay_and_compare(run, xs)

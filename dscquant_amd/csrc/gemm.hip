@@ -272,9 +272,11 @@ __global__ __launch_bounds__(64 * WM * WN) void w4a4_gemm_kernel(GemmArgs g) {
 // slice s).
 // Each step interleaves its MFMAs with the nibble unpack of the next step's
 // fragments.  The tile's row scales / zero-points are staged in LDS once.
-// The epilogue stores runs of 4 columns per lane straight from the
-// accumulators (N % 8 == 0; out and raw 16-byte aligned).  Row and column
-// metadata (sx, zx, sw, sums, bias) are staged in LDS with the first slice.
+// The epilogue (N % 8 == 0; out and raw 16-byte aligned) writes fp16 output
+// through LDS as whole 128-byte row segments; fp32 output and the raw
+// accumulators are stored as runs of 4 columns per lane straight from the
+// accumulators.  Row and column metadata (sx, zx, sw, sums, bias) are staged
+// in LDS with the first slice.
 
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -521,6 +523,51 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     return res;
   };
   OutT* out = static_cast<OutT*>(g.out);
+  // fp16 output without raw accumulators: each wave's TM x 64 tile passes
+  // through LDS (the slice buffers, idle once every wave is past the K loop)
+  // so that a store instruction writes 8 whole 128-byte row segments instead
+  // of 16-byte pieces of 32 rows (M=2048, N=4096: 2.1-2.6 us faster at every
+  // K; the 16 MiB of output then take ~3.2 us).  Rows in LDS are 128 bytes, 16-byte
+  // chunk c of row r stored at c ^ (r & 7), so 8 consecutive lanes -- 8 rows
+  // on the writes, one row on the reads -- cover all banks.  A wave reads back
+  // only what it wrote (its LDS accesses complete in order).
+  if constexpr (sizeof(OutT) == 2 && TN == 64) {
+    static_assert(WM * WN * TM * TN * 2 <= 2 * STAGE, "staged tiles fit the slice buffers");
+    if (!g.raw) {
+      __syncthreads();
+      uint8_t* const tile = smem + wave * (TM * TN * 2);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 sw = swc[j][q];
+            const int4 sm = sumc[j][q];
+            const float4 b = bc[j][q];
+            const __half h0 = to_out<__half>(value(i, j, 4 * q + 0, sw.x, sm.x, b.x));
+            const __half h1 = to_out<__half>(value(i, j, 4 * q + 1, sw.y, sm.y, b.y));
+            const __half h2 = to_out<__half>(value(i, j, 4 * q + 2, sw.z, sm.z, b.z));
+            const __half h3 = to_out<__half>(value(i, j, 4 * q + 3, sw.w, sm.w, b.w));
+            uint2 pk;
+            pk.x = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
+            pk.y = (uint32_t)__half_as_ushort(h2) | ((uint32_t)__half_as_ushort(h3) << 16);
+            const int lr = i * 32 + rl;
+            *reinterpret_cast<uint2*>(tile + lr * 128 + 16 * ((4 * j + q) ^ (rl & 7)) +
+                                      8 * (lane >> 5)) = pk;
+          }
+      const int c8 = lane & 7;
+      const int64_t col = n0 + wn * TN + 8 * c8;
+#pragma unroll
+      for (int s = 0; s < TM / 8; ++s) {
+        const int lr = 8 * s + (lane >> 3);
+        const uint4 v = *reinterpret_cast<const uint4*>(tile + lr * 128 + 16 * (c8 ^ (lr & 7)));
+        const int64_t row = m0 + wm * TM + lr;
+        if (row < g.M && col < g.N) *reinterpret_cast<uint4*>(out + row * g.N + col) = v;
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int64_t row = m0 + wm * TM + i * 32 + rl;

@@ -408,21 +408,29 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  // Row and column metadata of the tile, once per workgroup, loaded between
+  // the two slices: a wave's loads complete in issue order, so storing it to
+  // LDS before the first barrier waits for slice 0 but not for slice 1.  Every
+  // thread loads (indices clamped) so that no load sits behind a branch.
   uint4 G0[LOADS], G1[LOADS];
   gload(G0, 0);
+  const int64_t mrow = min(m0 + min(tid, BM - 1), g.arows - 1);
+  const int64_t mcol = min(n0 + min(tid, BN - 1), g.brows - 1);
+  const float meta_sx = g.sx[mrow], meta_sw = g.sw[mcol];
+  const int32_t meta_z = g.zx[mrow], meta_sum = g.sums[mcol];
+  const float meta_b =
+      BIAS ? (float)static_cast<const OutT*>(g.bias)[min(n0 + min(tid, BN - 1), g.N - 1)] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
   gload(G1, 1);
-  // Row and column metadata of the tile, once per workgroup (after the slice
-  // loads, so the first slice is not queued behind it).
+  __builtin_amdgcn_sched_barrier(0);
   if (tid < BM) {
-    const int64_t row = min(m0 + tid, g.arows - 1);
-    lds_sx[tid] = g.sx[row];
-    lds_z[tid] = 8 - g.zx[row];
+    lds_sx[tid] = meta_sx;
+    lds_z[tid] = 8 - meta_z;
   }
   if (tid < BN) {
-    const int64_t col = min(n0 + tid, g.brows - 1);
-    lds_sw[tid] = g.sw[col];
-    lds_sum[tid] = g.sums[col];
-    if (BIAS) lds_b[tid] = (float)static_cast<const OutT*>(g.bias)[min(n0 + tid, g.N - 1)];
+    lds_sw[tid] = meta_sw;
+    lds_sum[tid] = meta_sum;
+    if (BIAS) lds_b[tid] = meta_b;
   }
   lstore(G0, 0, C0{}, C3{});
   lds_barrier();

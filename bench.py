@@ -74,6 +74,10 @@ def parse():
     p.add_argument("--kernel-iters", type=int, default=100)
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="budget of the CPU baseline sample")
+    p.add_argument("--warm-seconds", type=float, default=2.0,
+                   help="run the workload's steps back to back this long before timing anything "
+                        "(from idle the GPU takes a few hundred milliseconds to reach its "
+                        "steady clock)")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-graph", action="store_true")
     p.add_argument("--kernels-only", action="store_true",
@@ -122,6 +126,47 @@ def time_kernel(launch, n, torch, dev):
     end.record()
     end.synchronize()
     return start.elapsed_time(end) / n * 1e-3  # seconds
+
+
+def time_in_steps(kernels, n, torch, lead=512):
+    """Average device time of each kernel of a step, measured inside n eager
+    steps with HIP events on the launch stream between consecutive kernels.
+    The kernels run in the mix the timed steps run them in (a GEMM right after
+    a quantize kernel) rather than a hundred launches of one kernel back to
+    back, whose sustained power draw lowers the clock; a kernel trace of the
+    bench command averages the same mix."""
+    nk = len(kernels)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(nk + 1)] for _ in range(n)]
+    torch.cuda.synchronize()
+    # A lead of untimed steps keeps the GPU busy while the host queues the timed
+    # ones, so no interval between two events waits for the host.
+    for i in range(lead):
+        for fn in kernels:
+            fn(i)
+    for i in range(n):
+        for k, fn in enumerate(kernels):
+            evs[i][k].record()
+            fn(i)
+        evs[i][nk].record()
+    torch.cuda.synchronize()
+    return [sum(evs[i][k].elapsed_time(evs[i][k + 1]) for i in range(n)) / n * 1e-3
+            for k in range(nk)]
+
+
+def warm_up(step, seconds, torch):
+    """Runs step(0), step(1), ... back to back for about `seconds`.  From idle the
+    GPU needs a few hundred milliseconds of sustained work to reach its steady
+    clock: the first few hundred GEMM launches of a fresh process run up to ~20%
+    slower than the ones after them."""
+    if seconds <= 0:
+        return
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(32):
+            step(i)
+            i += 1
+        torch.cuda.synchronize()
 
 
 COPY_BYTES = 16 << 20
@@ -235,7 +280,7 @@ def main():
         print(json.dumps(traffic_summary(*args.traffic), indent=1))
         return
     if args.vendor_int8:
-        return vendor_int8()
+        return vendor_int8(args.warm_seconds)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(this build runs the path on a single MI355X)", file=sys.stderr)
@@ -301,10 +346,14 @@ def main():
               f"{COPY_BYTES >> 20} MiB copy", flush=True)
         return
 
-    # ---- per-kernel device times (HIP events on the launch stream)
-    t_quant = time_kernel(lambda i: quantize(xs[i % nbuf]), args.kernel_iters, torch, dev)
+    # ---- per-kernel device times (HIP events on the launch stream): inside
+    # steps (the roofline figures) and, for reference, back to back
+    warm_up(step, args.warm_seconds, torch)
+    t_quant, t_gemm = time_in_steps([lambda i: quantize(xs[i % nbuf]), lambda i: gemm()],
+                                    args.kernel_iters, torch)
+    t_quant_iso = time_kernel(lambda i: quantize(xs[i % nbuf]), args.kernel_iters, torch, dev)
     quantize(xs[0])
-    t_gemm = time_kernel(lambda i: gemm(), args.kernel_iters, torch, dev)
+    t_gemm_iso = time_kernel(lambda i: gemm(), args.kernel_iters, torch, dev)
 
     # ---- whole steps.  Runs of up to GRAPH_STEPS consecutive steps are captured
     # into one HIP graph each, so the timed region is the GPU's own step time
@@ -367,11 +416,13 @@ def main():
         gemm_line = {"bound": "hbm", "achieved": round(gemm_gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gemm_gbs / PEAK_HBM_GBS, 4),
                      "kernel": "w4a4_gemv_kernel", "avg_us": round(t_gemm * 1e6, 3),
+                     "isolated_us": round(t_gemm_iso * 1e6, 3),
                      "bytes_per_launch": gbytes, "tops": round(gemm_tops, 2)}
     else:
         gemm_line = {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "kernel": "w4a4_gemm_pipe_kernel", "avg_us": round(t_gemm * 1e6, 3),
+                     "isolated_us": round(t_gemm_iso * 1e6, 3),
                      "ops_per_launch": ops, "algorithmic_bytes": M * K // 2 + N * K // 2 + 2 * M * N}
 
     traffic = load_traffic(args.workload)
@@ -401,7 +452,8 @@ def main():
         "kernels": {
             "quantize": {"bound": "hbm", "achieved": round(quant_gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(quant_gbs / PEAK_HBM_GBS, 4),
-                         "avg_us": round(t_quant * 1e6, 3), "bytes_per_launch": qbytes,
+                         "avg_us": round(t_quant * 1e6, 3),
+                         "isolated_us": round(t_quant_iso * 1e6, 3), "bytes_per_launch": qbytes,
                          "traffic": (traffic["quantize"]["traffic"]
                                      if traffic and "quantize" in traffic else None)},
             "gemm": gemm_line,
@@ -449,7 +501,7 @@ def run_graph_steps(args, torch, dev, step):
     return (time.perf_counter() - t0) / args.steps
 
 
-def vendor_int8():
+def vendor_int8(warm_seconds=2.0):
     """The platform library's dense int8 GEMM (hipBLASLt through torch._int_mm: int8
     operands, int32 result, no int4 unpacking, no epilogue) and fp16 matmul, as a
     reference point for the W4A4 kernel.  B is K-contiguous (the layout this build's
@@ -463,8 +515,7 @@ def vendor_int8():
         ah, bh = a.half(), b.half()
         for name, fn in (("int8 torch._int_mm", lambda: torch._int_mm(a, b)),
                          ("fp16 matmul", lambda: ah @ bh)):
-            fn()
-            torch.cuda.synchronize()
+            warm_up(lambda i: fn(), warm_seconds, torch)  # same warm-up as the W4A4 timings
             times = []
             for _ in range(5):
                 s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -541,6 +592,7 @@ def main_decode(args, torch, _lib, w4a4):
               f"{COPY_BYTES >> 20} MiB copy", flush=True)
         return
 
+    warm_up(step, args.warm_seconds, torch)
     t_two = time_kernel(two_launch, args.kernel_iters, torch, dev)
     t_quant = time_kernel(quantize, args.kernel_iters, torch, dev)
     quantize(0)
@@ -654,9 +706,11 @@ def main_mlp(args, torch, _lib, w4a4):
 
     step(0)
     torch.cuda.synchronize()
-    t = {name: time_kernel(fn, args.kernel_iters, torch, dev)
-         for name, fn in (("quantize", quantize), ("gemm_gate_up", gemm_gu),
-                          ("silu_mul_quantize", gated), ("gemm_down", gemm_down))}
+    warm_up(step, args.warm_seconds, torch)
+    names = ("quantize", "gemm_gate_up", "silu_mul_quantize", "gemm_down")
+    fns = (quantize, gemm_gu, gated, gemm_down)
+    t = dict(zip(names, time_in_steps(fns, args.kernel_iters, torch)))
+    t_iso = {name: time_kernel(fn, args.kernel_iters, torch, dev) for name, fn in zip(names, fns)}
     sec = run_graph_steps(args, torch, dev, step)
     ops = 2.0 * M * (2 * N) * K + 2.0 * M * K * N
     gu_ops = 2.0 * M * (2 * N) * K
@@ -666,6 +720,7 @@ def main_mlp(args, torch, _lib, w4a4):
             "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
             "frac": round(gu_ops / t["gemm_gate_up"] / 1e12 / PEAK_INT8_TOPS, 4),
             "kernel": "w4a4_gemm_pipe_kernel (gate|up)", "avg_us": round(t["gemm_gate_up"] * 1e6, 3),
+            "isolated_us": round(t_iso["gemm_gate_up"] * 1e6, 3),
             "ops_per_launch": gu_ops, "traffic": None}
     result = {
         "metric": METRIC, "value": round(ops / sec / 1e12, 2), "unit": "TOPS", "n_gpus": 1,
@@ -679,12 +734,15 @@ def main_mlp(args, torch, _lib, w4a4):
         "roofline": line,
         "kernels": {
             "quantize": {"bound": "hbm", "avg_us": round(t["quantize"] * 1e6, 3),
+                         "isolated_us": round(t_iso["quantize"] * 1e6, 3),
                          "achieved": round(qbytes / t["quantize"] / 1e9, 1), "unit": "GB/s"},
             "gemm_gate_up": dict(line),
             "silu_mul_quantize": {"bound": "hbm", "avg_us": round(t["silu_mul_quantize"] * 1e6, 3),
+                                  "isolated_us": round(t_iso["silu_mul_quantize"] * 1e6, 3),
                                   "achieved": round(gbytes / t["silu_mul_quantize"] / 1e9, 1),
                                   "unit": "GB/s"},
             "gemm_down": {"bound": "mfma", "avg_us": round(t["gemm_down"] * 1e6, 3),
+                          "isolated_us": round(t_iso["gemm_down"] * 1e6, 3),
                           "achieved": round(2.0 * M * K * N / t["gemm_down"] / 1e12, 2),
                           "unit": "TOPS"},
         },

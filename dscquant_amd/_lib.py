@@ -27,6 +27,7 @@ _P, _I, _I64, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
     "dscq_quantize": [_P, _I, _I64, _I64, _F, _I, _I, _P, _P, _P, _P, _P],
     "dscq_silu_mul_quantize": [_P, _P, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P],
+    "dscq_matmul_silu_mul": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P],
     "dscq_activation_codes": [_P, _I, _I64, _I64, _F, _I, _I, _P, _P, _P, _P],
     "dscq_pack_weight": [_P, _I, _I64, _I64, _F, _I, _P, _P, _P, _P, _P],
     "dscq_weight_codes": [_P, _I, _I64, _I64, _F, _I, _I, _P, _P, _P],

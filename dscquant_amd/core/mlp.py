@@ -4,17 +4,20 @@ The reference quantizes each projection of a Llama MLP through its own
 QuantLinear (core/linear.py:48-52; core/model_ops.py drives the model) and
 runs the activation in between unquantized in torch.  ``QuantMLP`` keeps the
 three QuantLinear modules (their weights, clips, folds and rotations) and
-runs the block in three launches:
+runs the block in four launches:
 
     quantize(x)                                  -> packed x        (HIP)
-    matmul(packed x, [gate | up] weights)        -> gate|up [M, 2N] (HIP)
-    silu_mul_quantize(gate|up)                   -> packed h        (HIP)
+    matmul_silu_mul(packed x, gate/up weights)   -> h [M, N]        (HIP)
+    quantize(h)                                  -> packed h        (HIP)
     matmul(packed h, down weights)               -> out             (HIP)
 
 gate and up read the same quantized x, so they run as one GEMM against the
-row-concatenated packed weights; the SiLU, the product and the down
-projection's input quantization (with its online rotation) are one kernel.
-h follows an fp16 model's roundings: fp16(fp16(silu(g)) * u).
+packed weights interleaved in 64-row blocks, whose epilogue computes
+h = fp16(fp16(silu(g)) * u) (an fp16 model's roundings) from the two halves
+of each output tile.  When N is not a multiple of 64 the gate|up GEMM writes
+[M, 2N] against the row-concatenated weights instead, and one kernel applies
+the SiLU, the product and the down projection's input quantization
+(silu_mul_quantize); both give the same h and the same packed h.
 """
 from __future__ import annotations
 
@@ -59,16 +62,23 @@ class QuantMLP(nn.Module):
         pu, swu, su = self.up.packed_weight()
         _, bg = self.gate.transformed()
         _, bu = self.up.transformed()
+        N = self.gate.base.weight.shape[0]
         bias = None
         if bg is not None or bu is not None:
-            N = self.gate.base.weight.shape[0]
             zero = torch.zeros(N, dtype=torch.float16, device=pg.device)
-            bias = torch.cat([zero if bg is None else bg.detach().half(),
-                              zero if bu is None else bu.detach().half()])
+            bias = (zero if bg is None else bg.detach().half(),
+                    zero if bu is None else bu.detach().half())
+        # gate and up rows interleaved in 64-row blocks for matmul_silu_mul,
+        # else concatenated for the [M, 2N] GEMM + silu_mul_quantize
+        join = w4a4.interleave_gate_up if self._gated_gemm() else (lambda a, b: torch.cat([a, b]))
         pd, swd, sd = self.down.packed_weight()
-        self._packed = (key, torch.cat([pg, pu]), torch.cat([swg, swu]), torch.cat([sg, su]),
-                        bias, pd, swd, sd)
+        self._packed = (key, join(pg, pu), join(swg, swu), join(sg, su),
+                        None if bias is None else join(*bias), pd, swd, sd)
         return self._packed[1:]
+
+    def _gated_gemm(self) -> bool:
+        """Whether gate and up run as one GEMM with the SiLU-gated epilogue."""
+        return self.gate.base.weight.shape[0] % 64 == 0
 
     def forward(self, x):
         if not self._fusable():
@@ -101,8 +111,12 @@ class QuantMLP(nn.Module):
             if m == 0:
                 break
             pa, sx, zx = w4a4.quantize(part, aclip, True, rot_in)
-            gu, _ = w4a4.matmul(pa, pgu, sx, zx, swgu, sgu, bgu, m, 2 * N, True, False, False)
-            ph, sh, zh = w4a4.silu_mul_quantize(gu, dclip, rot_down)
+            if self._gated_gemm():
+                h = w4a4.matmul_silu_mul(pa, pgu, sx, zx, swgu, sgu, bgu, m, N)
+                ph, sh, zh = w4a4.quantize(h, dclip, True, rot_down)
+            else:
+                gu, _ = w4a4.matmul(pa, pgu, sx, zx, swgu, sgu, bgu, m, 2 * N, True, False, False)
+                ph, sh, zh = w4a4.silu_mul_quantize(gu, dclip, rot_down)
             o, _ = w4a4.matmul(ph, pd, sh, zh, swd, sd, bdown, m, NO, True, False, fp32)
             out[r0:r0 + m] = o
         return out.reshape(*lead, NO).to(x.dtype)

@@ -27,6 +27,11 @@ int w4a4_gemm(const uint8_t* a, const uint8_t* b, const float* sx, const int32_t
               const float* sw, const int32_t* sums, const void* bias, int64_t M,
               int64_t N, int64_t KP, bool decode, bool out_fp32, void* out,
               int32_t* raw, hipStream_t stream);
+bool gemm_silu_mul_fits(int64_t M, int64_t NH, int64_t KP, const void* h);
+int w4a4_gemm_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
+                       const int32_t* zx, const float* sw, const int32_t* sums,
+                       const void* bias, int64_t M, int64_t NH, int64_t KP, void* h,
+                       hipStream_t stream);
 bool linear_decode_fits(int64_t M, int64_t K);
 int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, int rotate_block,
                   const uint8_t* b, const float* sw, const int32_t* sums, const void* bias,
@@ -140,6 +145,20 @@ int dscq_silu_mul_quantize(const void* gate, const void* up, int64_t ld, int64_t
   if (!gate || !up || !packed || !scales || !zeros) return fail("silu_mul_quantize: null buffer");
   return silu_mul_quant(gate, up, ld, M, N, ceil_to(M, 8), clip, rotate_block, packed, scales,
                         zeros, h, static_cast<hipStream_t>(stream));
+}
+
+int dscq_matmul_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
+                         const int32_t* zx, const float* sw, const int32_t* sums,
+                         const void* bias, int64_t M, int64_t N, int64_t KP, void* h,
+                         void* stream) {
+  if (!(M > 0 && M <= 65535)) return fail("matmul_silu_mul: require 1<=M<=65535");
+  if (!a || !b_gu || !sx || !zx || !sw || !sums || !h) return fail("matmul_silu_mul: null buffer");
+  if (!gemm_silu_mul_fits(M, N, KP, h))
+    return fail("matmul_silu_mul: need N %% 64 == 0, KP %% 64 == 0, KP <= 65536, 16-byte "
+                "aligned h (M=%lld, N=%lld, KP=%lld)", (long long)M, (long long)N,
+                (long long)KP);
+  return w4a4_gemm_silu_mul(a, b_gu, sx, zx, sw, sums, bias, M, N, KP, h,
+                            static_cast<hipStream_t>(stream));
 }
 
 int dscq_activation_codes(const void* x, int x_dtype, int64_t M, int64_t K, float clip,

@@ -42,6 +42,7 @@
 #include "../../include/dscq.h"
 #include "common.h"
 #include "mma_int4.h"
+#include "rowquant.h"
 
 namespace dscq {
 namespace {
@@ -282,7 +283,8 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <typename OutT, int BM, int BN, int WM, int WN, int MINB, bool KTAIL, bool BIAS>
+template <typename OutT, int BM, int BN, int WM, int WN, int MINB, bool KTAIL, bool BIAS,
+          bool GATED = false>
 __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(GemmArgs g) {
   constexpr int THREADS = 64 * WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32, NF = FM + FN;
@@ -564,6 +566,33 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
             *reinterpret_cast<uint2*>(tile + lr * 128 + 16 * ((4 * j + q) ^ (rl & 7)) +
                                       8 * (lane >> 5)) = pk;
           }
+      if constexpr (GATED) {
+        // SiLU-gated MLP (weights interleaved in 64-row blocks: gate rows then
+        // up rows of the same 64 outputs): the gate half of the tile's rows
+        // is in the LDS tiles of waves (wm, 0), the up half in (wm, 1).  Wave
+        // (wm, wn) combines rows wn * TM/2 .. +TM/2 of its row group into
+        // h = silu_mul_f16x2(g, u) -- the requantizing kernel's arithmetic --
+        // at h columns n0 / 2 .. +63 of the [M, N/2] output.
+        static_assert(WN == 2, "gated epilogue: gate in wave column 0, up in column 1");
+        __syncthreads();
+        const uint8_t* const gate_t = smem + (wm * WN + 0) * (TM * TN * 2);
+        const uint8_t* const up_t = smem + (wm * WN + 1) * (TM * TN * 2);
+        const int c8 = lane & 7;
+        const int64_t NH = g.N / 2;
+        const int64_t hcol = n0 / 2 + 8 * c8;
+#pragma unroll
+        for (int s = 0; s < TM / 16; ++s) {
+          const int lr = wn * (TM / 2) + 8 * s + (lane >> 3);
+          const int off = lr * 128 + 16 * (c8 ^ (lr & 7));
+          const uint4 gv = *reinterpret_cast<const uint4*>(gate_t + off);
+          const uint4 uv = *reinterpret_cast<const uint4*>(up_t + off);
+          const uint4 hv = make_uint4(silu_mul_f16x2(gv.x, uv.x), silu_mul_f16x2(gv.y, uv.y),
+                                      silu_mul_f16x2(gv.z, uv.z), silu_mul_f16x2(gv.w, uv.w));
+          const int64_t row = m0 + wm * TM + lr;
+          if (row < g.M && hcol < NH) *reinterpret_cast<uint4*>(out + row * NH + hcol) = hv;
+        }
+        return;
+      }
       const int c8 = lane & 7;
       const int64_t col = n0 + wn * TN + 8 * c8;
 #pragma unroll
@@ -611,7 +640,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   }
 }
 
-template <typename OutT, int BM, int BN, int WM, int WN, int MINB>
+template <typename OutT, int BM, int BN, int WM, int WN, int MINB, bool GATED = false>
 int launch_pipe_cfg(GemmArgs g, hipStream_t stream) {
   g.tiles_n = (int)((g.N + BN - 1) / BN);
   const int64_t nblocks = ((g.M + BM - 1) / BM) * g.tiles_n;
@@ -619,7 +648,8 @@ int launch_pipe_cfg(GemmArgs g, hipStream_t stream) {
   const bool ktail = (g.KP / 2) % 128 != 0;  // rows end inside a 128-byte slice
   const dim3 grid((unsigned)nblocks), block(64 * WM * WN);
 #define DSCQ_PIPE(KT, BI)                                                                  \
-  hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<OutT, BM, BN, WM, WN, MINB, KT, BI>), grid, block, \
+  hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<OutT, BM, BN, WM, WN, MINB, KT, BI, GATED>), grid,   \
+                     block,                                                                    \
                      0, stream, g)
   if (g.bias) {
     if (ktail) DSCQ_PIPE(true, true); else DSCQ_PIPE(false, true);
@@ -654,16 +684,17 @@ int cu_count() {
 // spread the work over every CU (M=512, N=22016: 1.34 rounds of 256 x 128 and
 // 128 x 128 measure the same; M=512, N=4096, K=11008: 64 x 128 is 22% faster
 // than 128 x 128 and 37% faster than a quarter-full round of 256 x 128).
-template <typename OutT>
+template <typename OutT, bool GATED = false>
 int launch_pipe(GemmArgs g, hipStream_t stream) {
   const int64_t cus = cu_count();
   const int64_t tn = (g.N + 127) / 128;
   const int64_t t256 = ((g.M + 255) / 256) * tn;
   const int64_t last = t256 % cus;
   if ((t256 >= cus && (last == 0 || 10 * last > 6 * cus)) || (t256 < cus && 10 * t256 >= 6 * cus))
-    return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
-  if (((g.M + 127) / 128) * tn >= cus) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
-  return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2>(g, stream);
+    return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1, GATED>(g, stream);
+  if (((g.M + 127) / 128) * tn >= cus)
+    return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2, GATED>(g, stream);
+  return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2, GATED>(g, stream);
 }
 
 template <typename OutT, int BM, int BN, int WM, int WN, bool HUGE>
@@ -688,10 +719,15 @@ int launch_cfg(GemmArgs g, hipStream_t stream) {
 // Partial 16 x 16 sums meet in LDS; the epilogue is the reference's.
 // Bytes per launch: N * KP / 2 (weights) + the small A, read once per column
 // block from L2.
-template <typename OutT, bool BIAS>
+// GATED (dscq_matmul_silu_mul at M <= 16): output column n of h [M, N / 2]
+// takes weight row 128 (n / 64) + n % 64 (gate) and that row + 64 (up); both
+// are streamed by the same workgroup and combined in the epilogue with the
+// gated epilogue's silu_mul_f16x2.
+template <typename OutT, bool BIAS, bool GATED = false>
 __global__ __launch_bounds__(512) void w4a4_gemv_kernel(GemmArgs g) {
   constexpr int WAVES = 8;
-  __shared__ int32_t part[WAVES][16][16];
+  constexpr int NB = GATED ? 2 : 1;  // weight row streams (gate, up)
+  __shared__ int32_t part[NB][WAVES][16][16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t n0 = (int64_t)blockIdx.x * 16, m0 = (int64_t)blockIdx.y * 16;
   const int r = lane & 15, grp = lane >> 4;
@@ -699,21 +735,41 @@ __global__ __launch_bounds__(512) void w4a4_gemv_kernel(GemmArgs g) {
   const int64_t nblk = (KB + 63) / 64;
   const int64_t per = (nblk + WAVES - 1) / WAVES;
   const int64_t b0 = wave * per, b1 = min(b0 + per, nblk);
+  const int64_t NOUT = GATED ? g.N / 2 : g.N;  // output columns
+  auto wrow = [&](int64_t n, int s) -> int64_t {
+    return GATED ? 128 * (n / 64) + n % 64 + 64 * s : n;
+  };
   const uint8_t* arow = g.a + min(m0 + r, g.arows - 1) * KB;
-  const uint8_t* brow = g.b + min(n0 + r, g.brows - 1) * KB;
+  const uint8_t* brow[NB];
+#pragma unroll
+  for (int s = 0; s < NB; ++s) brow[s] = g.b + min(wrow(n0 + r, s), g.brows - 1) * KB;
   const int64_t off = grp * 16;
 
   // Epilogue operands of output (m0 + tid / 16 % 16, n0 + tid % 16), fetched
   // up front by every thread (indices clamped; only threads < 256 use them) so
   // that the epilogue does not wait for a second trip to memory.
   const int ml = (tid >> 4) & 15, nl = tid & 15;
-  const int64_t mc = min(m0 + ml, g.arows - 1), nc = min(n0 + nl, g.brows - 1);
-  const float e_sx = g.sx[mc], e_sw = g.sw[nc];
-  const int32_t e_z = 8 - g.zx[mc], e_sum = g.sums[nc];
-  const float e_b = BIAS ? (float)static_cast<const OutT*>(g.bias)[min(n0 + nl, g.N - 1)] : 0.0f;
+  const int64_t mc = min(m0 + ml, g.arows - 1), nout = min(n0 + nl, NOUT - 1);
+  const float e_sx = g.sx[mc];
+  const int32_t e_z = 8 - g.zx[mc];
+  float e_sw[NB], e_b[NB];
+  int32_t e_sum[NB];
+#pragma unroll
+  for (int s = 0; s < NB; ++s) {
+    const int64_t nc = min(GATED ? wrow(nout, s) : n0 + nl, g.brows - 1);
+    e_sw[s] = g.sw[nc];
+    e_sum[s] = g.sums[nc];
+    e_b[s] = BIAS ? (float)static_cast<const OutT*>(g.bias)[min(wrow(nout, s), g.N - 1)] : 0.0f;
+  }
 
-  v4i acc = {0, 0, 0, 0};
-  int32_t tot[4] = {0, 0, 0, 0};
+  v4i acc[NB];
+  int32_t tot[NB][4];
+#pragma unroll
+  for (int s = 0; s < NB; ++s) {
+    acc[s] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tot[s][v] = 0;
+  }
   auto piece = [&](const uint8_t* row, int64_t kb) {
     // The last block of a row with KB % 64 == 32 is half empty: its upper
     // pieces re-read the row's last piece and are zeroed.
@@ -722,64 +778,80 @@ __global__ __launch_bounds__(512) void w4a4_gemv_kernel(GemmArgs g) {
     if (!in) v = make_uint4(0u, 0u, 0u, 0u);
     return v;
   };
+  auto mfma2 = [&](const uint4& a4, const uint4& b4, v4i& c) {
+    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(a4.x, a4.y), unpack8(b4.x, b4.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(a4.z, a4.w), unpack8(b4.z, b4.w), c, 0, 0, 0);
+  };
   constexpr int U = 4;  // blocks in flight per wave
   int64_t blk = b0;
   for (; blk + U <= b1; blk += U) {
-    uint4 av[U], bv[U];
+    uint4 av[U], bv[NB][U];
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       av[i] = piece(arow, (blk + i) * 64);
-      bv[i] = piece(brow, (blk + i) * 64);
+#pragma unroll
+      for (int s = 0; s < NB; ++s) bv[s][i] = piece(brow[s], (blk + i) * 64);
     }
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(av[i].x, av[i].y),
-                                                  unpack8(bv[i].x, bv[i].y), acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(av[i].z, av[i].w),
-                                                  unpack8(bv[i].z, bv[i].w), acc, 0, 0, 0);
-    }
+    for (int i = 0; i < U; ++i)
+#pragma unroll
+      for (int s = 0; s < NB; ++s) mfma2(av[i], bv[s][i], acc[s]);
     // |partial| <= 2^14 per product: drain every 65536 k (512 blocks).
     if (((blk - b0) / U + 1) % (512 / U) == 0) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) tot[v] += acc[v] >> 8;
-      acc = v4i{0, 0, 0, 0};
+      for (int s = 0; s < NB; ++s) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tot[s][v] += acc[s][v] >> 8;
+        acc[s] = v4i{0, 0, 0, 0};
+      }
     }
   }
   for (; blk < b1; ++blk) {
-    const uint4 a4 = piece(arow, blk * 64), b4 = piece(brow, blk * 64);
-    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(a4.x, a4.y), unpack8(b4.x, b4.y), acc,
-                                                0, 0, 0);
-    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(a4.z, a4.w), unpack8(b4.z, b4.w), acc,
-                                                0, 0, 0);
+    const uint4 a4 = piece(arow, blk * 64);
+#pragma unroll
+    for (int s = 0; s < NB; ++s) mfma2(a4, piece(brow[s], blk * 64), acc[s]);
   }
   // D of a 16 x 16 tile: row (A) 4 * (lane / 16) + v, column (B) lane % 16.
 #pragma unroll
-  for (int v = 0; v < 4; ++v) part[wave][4 * grp + v][r] = tot[v] + (acc[v] >> 8);
+  for (int s = 0; s < NB; ++s)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[s][wave][4 * grp + v][r] = tot[s][v] + (acc[s][v] >> 8);
   __syncthreads();
   if (tid >= 256) return;
-  int32_t raw = 0;
+  int32_t raw[NB];
+  float res[NB];
 #pragma unroll
-  for (int w = 0; w < WAVES; ++w) raw += part[w][ml][nl];
+  for (int s = 0; s < NB; ++s) {
+    raw[s] = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) raw[s] += part[s][w][ml][nl];
+    // Operation order of kernel/w4a4.cu:74-77.
+    const int32_t corrected = raw[s] + e_z * e_sum[s];
+    res[s] = (float)corrected * e_sx;
+    res[s] = res[s] * e_sw[s];
+    if (BIAS) res[s] = res[s] + e_b[s];
+  }
   const int64_t m = m0 + ml, n = n0 + nl;
-  if (m >= g.M || n >= g.N) return;
-  // Operation order of kernel/w4a4.cu:74-77.
-  const int32_t corrected = raw + e_z * e_sum;
-  float res = (float)corrected * e_sx;
-  res = res * e_sw;
-  if (BIAS) res = res + e_b;
-  static_cast<OutT*>(g.out)[m * g.N + n] = to_out<OutT>(res);
-  if (g.raw) g.raw[m * g.N + n] = raw;
+  if (m >= g.M || n >= NOUT) return;
+  if constexpr (GATED) {
+    const uint32_t gb = __half_as_ushort(to_out<__half>(res[0]));
+    const uint32_t ub = __half_as_ushort(to_out<__half>(res[1]));
+    static_cast<uint16_t*>(g.out)[m * NOUT + n] = (uint16_t)(silu_mul_f16x2(gb, ub) & 0xFFFFu);
+  } else {
+    static_cast<OutT*>(g.out)[m * g.N + n] = to_out<OutT>(res[0]);
+    if (g.raw) g.raw[m * g.N + n] = raw[0];
+  }
 }
 
-template <typename OutT>
+template <typename OutT, bool GATED = false>
 int launch_gemv(GemmArgs g, hipStream_t stream) {
-  const int64_t gx = (g.N + 15) / 16, gy = (g.M + 15) / 16;
+  const int64_t gx = ((GATED ? g.N / 2 : g.N) + 15) / 16, gy = (g.M + 15) / 16;
   if (gx > 0x7FFFFFFF || gy > 65535) return fail("matmul: grid too large");
   const dim3 grid((unsigned)gx, (unsigned)gy), block(512);
   if (g.bias)
-    hipLaunchKernelGGL((w4a4_gemv_kernel<OutT, true>), grid, block, 0, stream, g);
+    hipLaunchKernelGGL((w4a4_gemv_kernel<OutT, true, GATED>), grid, block, 0, stream, g);
   else
-    hipLaunchKernelGGL((w4a4_gemv_kernel<OutT, false>), grid, block, 0, stream, g);
+    hipLaunchKernelGGL((w4a4_gemv_kernel<OutT, false, GATED>), grid, block, 0, stream, g);
   return launch_status("w4a4_gemv_kernel");
 }
 
@@ -855,6 +927,45 @@ int w4a4_gemm(const uint8_t* a, const uint8_t* b, const float* sx, const int32_t
   g.tiles_n = 0;
   return out_fp32 ? gemm_typed<float>(g, decode, stream)
                   : gemm_typed<__half>(g, decode, stream);
+}
+
+// The gated GEMM's shape requirements (the caller reports them): h columns a
+// multiple of 64, KP <= 65536 (the pipelined kernel's accumulator range),
+// 32-bit row offsets, 16-byte aligned h.
+bool gemm_silu_mul_fits(int64_t M, int64_t NH, int64_t KP, const void* h) {
+  const int64_t KB = KP / 2;
+  return M >= 1 && NH >= 64 && NH % 64 == 0 && KP >= 64 && KP % 64 == 0 && KP <= 65536 &&
+         ceil_to(M, 8) * KB <= 0xFFFFFFFFll && 2 * NH * KB <= 0xFFFFFFFFll &&
+         (reinterpret_cast<uintptr_t>(h) & 15) == 0;
+}
+
+// h[M, NH] = fp16(fp16(silu(g)) * u) of the gate and up projections of one
+// SiLU-gated MLP, from one GEMM against b_gu: 2 * NH packed weight rows
+// interleaved in 64-row blocks (block t: gate rows 64t..64t+63, then up rows
+// 64t..64t+63), with sw, sums (and bias, fp16, when given) in the same order.
+int w4a4_gemm_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
+                       const int32_t* zx, const float* sw, const int32_t* sums,
+                       const void* bias, int64_t M, int64_t NH, int64_t KP, void* h,
+                       hipStream_t stream) {
+  GemmArgs g;
+  g.a = a;
+  g.b = b_gu;
+  g.sx = sx;
+  g.zx = zx;
+  g.sw = sw;
+  g.sums = sums;
+  g.bias = bias;
+  g.out = h;
+  g.raw = nullptr;
+  g.M = M;
+  g.N = 2 * NH;
+  g.KP = KP;
+  g.arows = ceil_to(M, 8);
+  g.brows = 2 * NH;
+  g.tiles_n = 0;
+  // Few tokens: the skinny-M kernel streams each weight row once.
+  if (M <= 16) return launch_gemv<__half, true>(g, stream);
+  return launch_pipe<__half, true>(g, stream);
 }
 
 }  // namespace dscq

@@ -103,25 +103,7 @@ __device__ __forceinline__ void write_row_meta(const RowArgs& a, int64_t row, bo
 // FULL: every chunk of every quad lies inside K (K == nblk * 128 and
 // nblk == 16 * WPR * ITERS), so no per-chunk masking is needed.
 // Gated input (the SiLU-gated MLP between its up and down projections): the
-// row is h = fp16(fp16(silu(g)) * u) of two fp16 rows g (x) and u (up), the
-// roundings an fp16 model applies to act_fn(gate) and to the product.
-// silu(g) = g / (1 + e^-g) is evaluated with the hardware exp2 and reciprocal
-// (a few fp32 ulps), far inside the fp16 rounding that follows; exp's last
-// bit differs between math libraries anyway.  g -> -inf gives e^-g = inf and
-// g * rcp(inf) = -0, the limit.
-__device__ __forceinline__ uint32_t silu_mul_f16x2(uint32_t g2, uint32_t u2) {
-  uint32_t h2 = 0;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float g = h2f((g2 >> (16 * i)) & 0xFFFFu);
-    const float u = h2f((u2 >> (16 * i)) & 0xFFFFu);
-    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
-    const float sg = __half2float(__float2half_rn(g * __builtin_amdgcn_rcpf(1.0f + e)));
-    const __half h = __float2half_rn(sg * u);
-    h2 |= (uint32_t)__half_as_ushort(h) << (16 * i);
-  }
-  return h2;
-}
+// row is h = silu_mul_f16x2(g, u) (rowquant.h) of two fp16 rows g (x) and u (up).
 
 template <typename T, bool ROT, int MODE, int WPR, int ITERS, bool FULL, bool GATED = false>
 __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {

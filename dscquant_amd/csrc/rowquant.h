@@ -68,6 +68,27 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)bits16));
 }
 
+// SiLU-gated MLP activation of two fp16 pairs: h = fp16(fp16(silu(g)) * u),
+// the roundings an fp16 model applies to act_fn(gate) and to the product.
+// silu(g) = g / (1 + e^-g) is evaluated with the hardware exp2 and reciprocal
+// (a few fp32 ulps), far inside the fp16 rounding that follows; exp's last
+// bit differs between math libraries anyway.  g -> -inf gives e^-g = inf and
+// g * rcp(inf) = -0, the limit.  Used by the requantizing kernel and by the
+// GEMM's gated epilogue, so both give the same h.
+__device__ __forceinline__ uint32_t silu_mul_f16x2(uint32_t g2, uint32_t u2) {
+  uint32_t h2 = 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float g = h2f((g2 >> (16 * i)) & 0xFFFFu);
+    const float u = h2f((u2 >> (16 * i)) & 0xFFFFu);
+    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+    const float sg = __half2float(__float2half_rn(g * __builtin_amdgcn_rcpf(1.0f + e)));
+    const __half h = __float2half_rn(sg * u);
+    h2 |= (uint32_t)__half_as_ushort(h) << (16 * i);
+  }
+  return h2;
+}
+
 // Zero the values of a chunk that was loaded from the placeholder address.
 template <typename T>
 __device__ __forceinline__ void mask_f32(bool ok, float v[8]) {

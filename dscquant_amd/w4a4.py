@@ -26,7 +26,8 @@ import torch
 from . import _lib
 
 __all__ = ["quantize", "matmul", "pack_weight", "silu_mul_quantize", "linear_decode",
-           "linear_decode_supported", "padded", "check_quantize_args", "check_matmul_args"]
+           "linear_decode_supported", "matmul_silu_mul", "interleave_gate_up", "padded",
+           "check_quantize_args", "check_matmul_args"]
 
 
 def padded(v: int, m: int) -> int:
@@ -248,3 +249,45 @@ def silu_mul_quantize(gate_up: torch.Tensor, clip: float = 1.0, rotate_block: in
     if return_h:
         out.append(h)
     return out
+
+
+def interleave_gate_up(gate, up, block: int = 64) -> torch.Tensor:
+    """Rows of two [N, ...] tensors (packed weights, sw, sums or bias of a gate and
+    an up projection) interleaved in ``block``-row blocks, the weight order
+    ``matmul_silu_mul`` reads: gate rows 64t .. 64t+63, then up rows 64t .. 64t+63."""
+    if gate.shape != up.shape or gate.size(0) % block:
+        raise RuntimeError(f"interleave_gate_up: need equal shapes with rows % {block} == 0")
+    rest = tuple(gate.shape[1:])
+    g = gate.reshape(gate.size(0) // block, block, *rest)
+    u = up.reshape(up.size(0) // block, block, *rest)
+    return torch.stack([g, u], dim=1).reshape(2 * gate.size(0), *rest).contiguous()
+
+
+def matmul_silu_mul(a, b_gu, sx, zx, sw, sums, bias, M: int, N: int) -> torch.Tensor:
+    """h [M, N] fp16 = fp16(fp16(silu(g)) * u) of the gate and up projections in one
+    GEMM (include/dscq.h: dscq_matmul_silu_mul).  ``a``, ``sx``, ``zx`` as for
+    ``matmul``; ``b_gu``, ``sw``, ``sums`` and ``bias`` (empty or fp16 [2N]) hold
+    the gate and up rows in ``interleave_gate_up`` order.  Needs N % 64 == 0."""
+    for t in (a, b_gu, sx, zx, sw, sums, bias):
+        _check_cuda(t)
+        if t.device != a.device:
+            raise RuntimeError("All buffers must be on the same device")
+    M, N = int(M), int(N)
+    if not (a.dim() == 2 and a.dtype == torch.uint8 and b_gu.dim() == 2
+            and b_gu.dtype == torch.uint8 and a.size(1) == b_gu.size(1)
+            and a.size(0) >= padded(M, 8) and b_gu.size(0) == 2 * N):
+        raise RuntimeError("Invalid padded operand shapes")
+    if not (sx.dtype == torch.float32 and zx.dtype == torch.int32 and sw.dtype == torch.float32
+            and sums.dtype == torch.int32 and sx.numel() >= padded(M, 8)
+            and zx.numel() >= padded(M, 8) and sw.numel() == 2 * N and sums.numel() == 2 * N):
+        raise RuntimeError("Invalid metadata dtypes")
+    if not (bias.numel() == 0 or (bias.dtype == torch.float16 and bias.numel() == 2 * N)):
+        raise RuntimeError("Bias shape/dtype mismatch")
+    dev = a.device
+    _lib.require_gfx950(dev)
+    h = torch.empty((M, N), dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("dscq_matmul_silu_mul", a.data_ptr(), b_gu.data_ptr(), sx.data_ptr(),
+                  zx.data_ptr(), sw.data_ptr(), sums.data_ptr(), _lib.ptr(bias), M, N,
+                  a.size(1) * 2, h.data_ptr(), _lib.stream(dev))
+    return h

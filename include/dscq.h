@@ -77,6 +77,30 @@ int dscq_silu_mul_quantize(const void* gate, const void* up, int64_t ld, int64_t
                            float* scales, int32_t* zeros, void* h, void* stream);
 
 /*
+ * The gate and up projections of a SiLU-gated MLP and the activation between
+ * them in one GEMM: h = fp16(fp16(silu(g)) * u) with g, u the fp16 outputs
+ * dscq_matmul(a, gate / up weights, ..., fused = 1) would give, and silu as
+ * in dscq_silu_mul_quantize (bit-identical h).  dscq_quantize(h, ...) then
+ * gives the down projection's input, as dscq_silu_mul_quantize does, without
+ * the [M, 2N] gate|up output going through HBM.  No reference counterpart
+ * exists: it replaces the gate and up QuantLinear calls of core/linear.py:48-52
+ * and the unquantized torch activation between them.
+ *   a, sx, zx  as dscq_matmul (the quantized MLP input, KP = ceil(K/64)*64).
+ *   b_gu       u8 [2N, KP/2]: gate and up weights packed as dscq_pack_weight
+ *              does, rows interleaved in 64-row blocks: rows 128t .. 128t+63
+ *              are gate rows 64t .. 64t+63, rows 128t+64 .. 128t+127 the up
+ *              rows 64t .. 64t+63.
+ *   sw, sums   f32 / i32 [2N] in the same row order; bias NULL or fp16 [2N]
+ *              in the same order (added to g and u before the activation).
+ *   h          out fp16 [M, N], 16-byte aligned.
+ * Limits: 1 <= M <= 65535, N % 64 == 0, KP <= 65536.
+ */
+int dscq_matmul_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
+                         const int32_t* zx, const float* sw, const int32_t* sums,
+                         const void* bias, int64_t M, int64_t N, int64_t KP, void* h,
+                         void* stream);
+
+/*
  * Activation codes with any bit width 2..8 (no packing), the GPU form of
  * activation_codes (core/quantization.py:13-21) on the padded layout.
  *   codes  out u8 [MP, KP] in [0, 2^bits - 1] (padded k / rows: the row's zero)

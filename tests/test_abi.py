@@ -274,3 +274,21 @@ def test_transformed_fold_rules():
     base_dn = torch.nn.Linear(16, 8)
     w, _ = QuantLinear(base_dn, cfg, scl, "down").transformed()
     torch.testing.assert_close(w, base_dn.weight * scl.s[None, :])
+
+
+def test_interleave_gate_up_order():
+    """Rows of gate and up interleaved in 64-row blocks (the gated GEMM's weight order)."""
+    import torch
+    from dscquant_amd import w4a4
+    N = 192
+    gate = torch.arange(N, dtype=torch.int32)
+    up = torch.arange(N, dtype=torch.int32) + 1000
+    il = w4a4.interleave_gate_up(gate, up)
+    expect = []
+    for t in range(N // 64):
+        expect += list(range(64 * t, 64 * t + 64)) + list(range(1000 + 64 * t, 1000 + 64 * t + 64))
+    assert il.tolist() == expect
+    g2, u2 = gate.reshape(N, 1).repeat(1, 3), up.reshape(N, 1).repeat(1, 3)
+    assert torch.equal(w4a4.interleave_gate_up(g2, u2)[:, 0], il)
+    with pytest.raises(RuntimeError):
+        w4a4.interleave_gate_up(gate[:100], up[:100])

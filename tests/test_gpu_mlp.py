@@ -59,6 +59,57 @@ class Cfg:
     activation_bits = 4
 
 
+def _deinterleave(gu_i, N):
+    """Columns of a GEMM against interleave_gate_up weights back to [gate | up]."""
+    M = gu_i.shape[0]
+    blocks = gu_i.reshape(M, N // 64, 2, 64)
+    return torch.cat([blocks[:, :, 0].reshape(M, N), blocks[:, :, 1].reshape(M, N)], dim=1)
+
+
+@pytest.mark.parametrize("M,K,N,bias", [(1, 4096, 11008, False), (5, 1088, 640, True),
+                                        (16, 4096, 2816, False), (17, 1000, 1024, True),
+                                        (64, 4096, 11008, False), (300, 1088, 64, True),
+                                        (512, 4096, 11008, True)])
+def test_matmul_silu_mul_matches_unfused_path(gpu, M, K, N, bias):
+    """The gated GEMM's h equals the [M, 2N] GEMM + silu_mul_quantize path's h bit
+    for bit (the skinny-M kernel for M <= 16, the tiled kernel above; K with a
+    partial last slice; gate/up bias), and quantize(h) its packed output."""
+    print(f"matmul_silu_mul case M{M} K{K} N{N} bias{bias}", flush=True)
+    x = torch.from_numpy(activations(M, K, seed=M + K)).to(gpu)
+    wg = torch.from_numpy(weights(N, K, seed=11)).to(gpu)
+    wu = torch.from_numpy(weights(N, K, seed=12)).to(gpu)
+    pg, swg, sg = w4a4.pack_weight(wg, 1.0, 0)
+    pu, swu, su = w4a4.pack_weight(wu, 1.0, 0)
+    gen = torch.Generator().manual_seed(N)
+    bg = (torch.randn(N, generator=gen) * 0.1).half().to(gpu) if bias else None
+    bu = (torch.randn(N, generator=gen) * 0.1).half().to(gpu) if bias else None
+    empty = torch.empty(0, dtype=torch.float16, device=gpu)
+    pa, sx, zx = w4a4.quantize(x, 1.0, True, 0)
+    gu, _ = w4a4.matmul(pa, torch.cat([pg, pu]), sx, zx, torch.cat([swg, swu]),
+                        torch.cat([sg, su]), torch.cat([bg, bu]) if bias else empty, M, 2 * N)
+    p_ref, s_ref, z_ref, h_ref = w4a4.silu_mul_quantize(gu, 1.0, 128 if N % 128 == 0 else 0,
+                                                        return_h=True)
+    il = w4a4.interleave_gate_up
+    h = w4a4.matmul_silu_mul(pa, il(pg, pu), sx, zx, il(swg, swu), il(sg, su),
+                             il(bg, bu) if bias else empty, M, N)
+    p, s_, z = w4a4.quantize(h, 1.0, True, 128 if N % 128 == 0 else 0)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h_ref)
+    assert torch.equal(p, p_ref) and torch.equal(s_, s_ref) and torch.equal(z, z_ref)
+
+
+def test_matmul_silu_mul_rejects_bad_shapes(gpu):
+    pa = torch.zeros((64, 64), dtype=torch.uint8, device=gpu)
+    sx = torch.ones(64, device=gpu)
+    zx = torch.zeros(64, dtype=torch.int32, device=gpu)
+    b = torch.zeros((192, 64), dtype=torch.uint8, device=gpu)  # N = 96: not a multiple of 64
+    sw = torch.ones(192, device=gpu)
+    sums = torch.zeros(192, dtype=torch.int32, device=gpu)
+    with pytest.raises(RuntimeError, match="N % 64 == 0"):
+        w4a4.matmul_silu_mul(pa, b, sx, zx, sw, sums, torch.empty(0, dtype=torch.float16,
+                                                                  device=gpu), 64, 96)
+
+
 def _linear(n_out, n_in, seed, gpu, bias=False):
     lin = torch.nn.Linear(n_in, n_out, bias=bias)
     with torch.no_grad():
@@ -97,6 +148,8 @@ def test_quant_mlp_matches_oracle(gpu, M, K, N, bias):
                         bgu_t if bgu_t is not None else torch.empty(0, dtype=torch.float16,
                                                                     device=gpu),
                         M, 2 * N, True, False, False)
+    if mlp._gated_gemm():  # weights interleaved in 64-row blocks: back to [gate | up]
+        gu = _deinterleave(gu, N)
     np.testing.assert_array_equal(gu.cpu().numpy(), gu_ref)
     _, _, _, h = w4a4.silu_mul_quantize(gu, 1.0, 128, return_h=True)
     bd = down.base.bias.cpu().numpy() if bias else None

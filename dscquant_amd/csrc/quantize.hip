@@ -57,34 +57,45 @@ struct RowArgs {
 // Outputs of one chunk: packed nibbles and / or codes.  Byte i of ev / od is
 // u = q (activations) or u = c + qmax + 1 (weights) for element 2i / 2i + 1.
 template <int MODE>
+__device__ __forceinline__ void store_codes(const RowArgs& a, int64_t row, int64_t e0,
+                                            uint32_t ev, uint32_t od);
+
+// Packed nibbles of 8 codes: act: (q - 8) & 15 == q ^ 8;  weight: c & 15 == (c + 8) ^ 8.
+__device__ __forceinline__ uint32_t packed_nibbles(uint32_t ev, uint32_t od) {
+  return (ev | (od << 4)) ^ 0x88888888u;
+}
+
+template <int MODE>
 __device__ __forceinline__ void store_chunk(const RowArgs& a, int64_t row,
                                             int64_t e0, uint32_t ev, uint32_t od) {
   if (e0 >= a.KP) return;
-  if (a.packed) {
-    // act: (q - 8) & 15 == q ^ 8;  weight: c & 15 == (c + 8) ^ 8.
-    const uint32_t p = (ev | (od << 4)) ^ 0x88888888u;
-    *reinterpret_cast<uint32_t*>(a.packed + row * (a.KP / 2) + e0 / 2) = p;
-  }
-  if (a.codes) {
-    uint32_t lo = __builtin_amdgcn_perm(od, ev, 0x05010400u);
-    uint32_t hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);
-    if (MODE == kWgt) {
-      // Per byte (no borrow between bytes): int8 code = u - (qmax + 1).
-      const uint32_t off = (uint32_t)(a.qmax + 1.0f);
-      uint32_t l2 = 0, h2 = 0;
+  if (a.packed)
+    *reinterpret_cast<uint32_t*>(a.packed + row * (a.KP / 2) + e0 / 2) = packed_nibbles(ev, od);
+  if (a.codes) store_codes<MODE>(a, row, e0, ev, od);
+}
+
+// The 8 codes unpacked, one byte each (the reference's two-step mode).
+template <int MODE>
+__device__ __forceinline__ void store_codes(const RowArgs& a, int64_t row, int64_t e0,
+                                            uint32_t ev, uint32_t od) {
+  uint32_t lo = __builtin_amdgcn_perm(od, ev, 0x05010400u);
+  uint32_t hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);
+  if (MODE == kWgt) {
+    // Per byte (no borrow between bytes): int8 code = u - (qmax + 1).
+    const uint32_t off = (uint32_t)(a.qmax + 1.0f);
+    uint32_t l2 = 0, h2 = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        l2 |= ((((lo >> (8 * i)) & 0xFFu) - off) & 0xFFu) << (8 * i);
-        h2 |= ((((hi >> (8 * i)) & 0xFFu) - off) & 0xFFu) << (8 * i);
-      }
-      lo = l2;
-      hi = h2;
+    for (int i = 0; i < 4; ++i) {
+      l2 |= ((((lo >> (8 * i)) & 0xFFu) - off) & 0xFFu) << (8 * i);
+      h2 |= ((((hi >> (8 * i)) & 0xFFu) - off) & 0xFFu) << (8 * i);
     }
-    uint2 w;
-    w.x = lo;
-    w.y = hi;
-    *reinterpret_cast<uint2*>(a.codes + row * a.KP + e0) = w;
+    lo = l2;
+    hi = h2;
   }
+  uint2 w;
+  w.x = lo;
+  w.y = hi;
+  *reinterpret_cast<uint2*>(a.codes + row * a.KP + e0) = w;
 }
 
 template <int MODE>
@@ -300,13 +311,35 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
   }
   if (!live) return;
 
+  // Row base computed once; e0 < KP <= 2^20 fits 32 bits; with FULL every
+  // chunk lies inside KP.  The unpacked codes (two-step mode) in their own
+  // uniform branch, so the packed stores are straight-line.
+  if (a.packed) {
+    uint8_t* const prow = a.packed + row * (a.KP / 2);
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    const int b = quad + it * NQ;
-    if (FULL || b < a.nblk) {
+    for (int it = 0; it < ITERS; ++it) {
+      const int b = quad + it * NQ;
+      if (FULL || b < a.nblk) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        store_chunk<MODE>(a, row, (int64_t)b * 128 + j * 32 + r * 8, ev[it][j], od[it][j]);
+        for (int j = 0; j < 4; ++j) {
+          const int e0 = b * 128 + j * 32 + r * 8;
+          if (FULL || e0 < a.KP)
+            *reinterpret_cast<uint32_t*>(prow + e0 / 2) = packed_nibbles(ev[it][j], od[it][j]);
+        }
+      }
+    }
+  }
+  if (a.codes) {
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int b = quad + it * NQ;
+      if (FULL || b < a.nblk) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int e0 = b * 128 + j * 32 + r * 8;
+          if (FULL || e0 < a.KP) store_codes<MODE>(a, row, e0, ev[it][j], od[it][j]);
+        }
+      }
     }
   }
   if (wave_in_row == 0 && lane == 0) write_row_meta<MODE>(a, row, real, rs, sum);

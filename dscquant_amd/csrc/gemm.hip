@@ -14,14 +14,15 @@
 // total every 65536 k.
 //
 // Kernels (dispatch in gemm_typed):
-//   w4a4_gemm_pipe_kernel  the main kernel (M >= 64, N % 8 == 0): 256-nibble
-//                          slices, swizzled LDS rows, two slices of global
-//                          loads in flight, one barrier per slice (its own
-//                          comment below);
-//   w4a4_gemv_kernel       M <= 16 or force_decode: weights streamed once,
-//                          K split over the waves of a workgroup;
-//   w4a4_gemm_kernel       everything else (16 < M < 64, N % 8 != 0, output not
-//                          16-byte aligned, KP > 65536): a simpler tiled kernel.
+//   w4a4_gemm_pipe_kernel  the main kernel (M >= 64, or 32 < M < 64 with N >= 8192;
+//                          N % 8 == 0): 256-nibble slices, swizzled LDS rows,
+//                          two slices of global loads in flight, one barrier
+//                          per slice (its own comment below);
+//   w4a4_gemv_kernel       M < 64 otherwise, or force_decode: weights streamed
+//                          once per 16 rows, K split over the waves of a
+//                          workgroup;
+//   w4a4_gemm_kernel       everything else (N % 8 != 0, output not 16-byte
+//                          aligned, KP > 65536 at M >= 64): a simpler tiled kernel.
 //
 // w4a4_gemm_kernel tiling.  A workgroup owns a BM x BN output tile; WM x WN
 // waves each own a (BM/WM) x (BN/WN) sub-tile made of 32 x 32
@@ -856,12 +857,17 @@ int launch_gemv(GemmArgs g, hipStream_t stream) {
 }
 
 // The pipelined kernel's layout requirements: whole 8-column groups, 16-byte
-// aligned output and raw rows, 64+ rows.
-bool pipe_ok(const GemmArgs& g) {
+// aligned output and raw rows, 32-bit row offsets.
+bool pipe_layout_ok(const GemmArgs& g) {
   auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
   const int64_t KB = g.KP / 2;
-  return g.N % 8 == 0 && g.M >= 64 && al(g.out, 16) && al(g.raw, 16) &&
-         g.arows * KB <= 0xFFFFFFFFll && g.brows * KB <= 0xFFFFFFFFll;
+  return g.N % 8 == 0 && al(g.out, 16) && al(g.raw, 16) && g.arows * KB <= 0xFFFFFFFFll &&
+         g.brows * KB <= 0xFFFFFFFFll;
+}
+bool pipe_ok(const GemmArgs& g) { return g.M >= 64 && pipe_layout_ok(g); }
+// 32 < M < 64 with N / 128 >= 64 tiles: the pipelined kernel over the skinny-M one.
+bool use_pipe_mid_m(const GemmArgs& g) {
+  return g.M > 32 && g.M < 64 && (g.N + 127) / 128 >= 64 && g.KP <= 65536 && pipe_layout_ok(g);
 }
 
 // DSCQ_GEMM_TILE=<BM>x<BN>[w8] pins the tile shape (tuning sweeps only).
@@ -869,7 +875,7 @@ template <typename OutT>
 int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
   static const char* env = getenv("DSCQ_GEMM_TILE");
   *handled = 1;
-  if (env && g.KP <= 65536 && (strncmp(env, "pipe", 4) != 0 || pipe_ok(g))) {
+  if (env && g.KP <= 65536 && (strncmp(env, "pipe", 4) != 0 || pipe_layout_ok(g))) {
     if (!strcmp(env, "128x256")) return launch_cfg<OutT, 128, 256, 2, 2, false>(g, stream);
     if (!strcmp(env, "128x128")) return launch_cfg<OutT, 128, 128, 2, 2, false>(g, stream);
     if (!strcmp(env, "256x128")) return launch_cfg<OutT, 256, 128, 2, 2, false>(g, stream);
@@ -895,8 +901,16 @@ int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
   const int rc = tile_override<OutT>(g, stream, &handled);
   if (handled) return rc;
   if (decode || g.M <= 16) return launch_gemv<OutT>(g, stream);
+  // 16 < M < 64: the skinny-M kernel streams the weights once per 16 rows but
+  // keeps every CU busy; the pipelined kernel's 64-row tiles pay off once the
+  // skinny kernel needs 3+ passes and N gives 64+ tiles (measured, M = 17..63:
+  // N = K = 4096 skinny 5.5-9.5 us vs pipelined 12.5 us; N = 11008, K = 4096:
+  // skinny 12.1 vs 12.7 us at M = 24, pipelined 12.9 vs 17.1 us at M = 40).
+  if (g.M < 64) {
+    if (use_pipe_mid_m(g)) return launch_pipe<OutT>(g, stream);
+    return launch_gemv<OutT>(g, stream);
+  }
   if (g.KP > 65536) return launch_cfg<OutT, 64, 64, 2, 2, true>(g, stream);
-  if (g.M <= 32) return launch_cfg<OutT, 32, 128, 1, 4, false>(g, stream);
   if (pipe_ok(g)) return launch_pipe<OutT>(g, stream);
   const int64_t big_tiles = ((g.M + 127) / 128) * ((g.N + 255) / 256);
   if (big_tiles >= 192) return launch_cfg<OutT, 128, 256, 2, 2, false>(g, stream);
@@ -963,8 +977,10 @@ int w4a4_gemm_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
   g.arows = ceil_to(M, 8);
   g.brows = 2 * NH;
   g.tiles_n = 0;
-  // Few tokens: the skinny-M kernel streams each weight row once.
-  if (M <= 16) return launch_gemv<__half, true>(g, stream);
+  // Few tokens: the skinny-M kernel streams each weight row once; up to 64
+  // rows it keeps doing so unless the pipelined kernel has 64+ tiles (as for
+  // dscq_matmul).
+  if (M <= 16 || (M < 64 && !use_pipe_mid_m(g))) return launch_gemv<__half, true>(g, stream);
   return launch_pipe<__half, true>(g, stream);
 }
 

@@ -685,6 +685,11 @@ int cu_count() {
 // spread the work over every CU (M=512, N=22016: 1.34 rounds of 256 x 128 and
 // 128 x 128 measure the same; M=512, N=4096, K=11008: 64 x 128 is 22% faster
 // than 128 x 128 and 37% faster than a quarter-full round of 256 x 128).
+// When a single round of 64 x 128 tiles covers the grid, eight waves of
+// 32 x 32 (two per SIMD) replace four of 32 x 64 (one per SIMD): with one wave
+// per SIMD each wave's LDS and load waits sit in series with its MFMAs
+// (measured: M=64..256, N=K=4096 12.7 -> 11.4-11.7 us; M=48, N=11008
+// 12.6 -> 11.1 us; slower once the tiles outnumber the CUs).
 template <typename OutT, bool GATED = false>
 int launch_pipe(GemmArgs g, hipStream_t stream) {
   const int64_t cus = cu_count();
@@ -695,6 +700,10 @@ int launch_pipe(GemmArgs g, hipStream_t stream) {
     return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1, GATED>(g, stream);
   if (((g.M + 127) / 128) * tn >= cus)
     return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2, GATED>(g, stream);
+  if constexpr (!GATED) {
+    if (((g.M + 63) / 64) * tn <= cus)
+      return launch_pipe_cfg<OutT, 64, 128, 2, 4, 2>(g, stream);
+  }
   return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2, GATED>(g, stream);
 }
 
@@ -888,6 +897,8 @@ int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
     if (!strcmp(env, "pipe128x256")) return launch_pipe_cfg<OutT, 128, 256, 2, 2, 1>(g, stream);
     if (!strcmp(env, "pipe128")) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
     if (!strcmp(env, "pipe64x128")) return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2>(g, stream);
+    if (!strcmp(env, "pipe64x128w8")) return launch_pipe_cfg<OutT, 64, 128, 2, 4, 2>(g, stream);
+    if (!strcmp(env, "pipe128x128w8")) return launch_pipe_cfg<OutT, 128, 128, 4, 2, 2>(g, stream);
     if (!strcmp(env, "pipe256x128w8")) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
     if (!strcmp(env, "pipe256x128")) return launch_pipe_cfg<OutT, 256, 128, 2, 2, 1>(g, stream);
   }

@@ -66,6 +66,10 @@ MM_CASES = [
     (96, 136, 128, True, False, False),
     (200, 264, 384, False, True, False),
     (256, 512, 4224, True, False, False),
+    # 64 x 128 tiles past one round (280 tiles): four waves per workgroup
+    (448, 5120, 512, True, False, False),
+    # mid-M with 65 column tiles and a K tail: eight-wave 64 x 128 tiles
+    (40, 8200, 320, True, False, False),
 ]
 
 

@@ -678,31 +678,38 @@ int cu_count() {
 
 // Tile choice.  256 x 128 tiles (one workgroup per CU, two waves per SIMD)
 // move the least data per MFMA and win whenever their rounds of one tile per
-// CU are well filled: a whole number of rounds, a last round more than 60%
-// full, or a single round over at least 60% of the CUs (measured: M=512,
-// N=11008 runs 13% faster on 172 CUs with 256 x 128 than on all of them with
-// 128 x 128).  Otherwise 128 x 128 or 64 x 128 tiles, two workgroups per CU,
-// spread the work over every CU (M=512, N=22016: 1.34 rounds of 256 x 128 and
-// 128 x 128 measure the same; M=512, N=4096, K=11008: 64 x 128 is 22% faster
-// than 128 x 128 and 37% faster than a quarter-full round of 256 x 128).
-// When a single round of 64 x 128 tiles covers the grid, eight waves of
-// 32 x 32 (two per SIMD) replace four of 32 x 64 (one per SIMD): with one wave
-// per SIMD each wave's LDS and load waits sit in series with its MFMAs
-// (measured: M=64..256, N=K=4096 12.7 -> 11.4-11.7 us; M=48, N=11008
-// 12.6 -> 11.1 us; slower once the tiles outnumber the CUs).
+// CU are well filled (a whole number of rounds, a last round more than 60%
+// full, or a single round over at least 60% of the CUs) and M wastes at most
+// an eighth more padded rows than 128-row tiles would (M=128, N=22016: 27.0 us
+// on 256-row tiles, 20.2 us on 128-row tiles; M=512, N=11008: 25.9 us on 172
+// CUs against 34 us on 128-row tiles over all of them).  Otherwise 128 x 128
+// or 64 x 128 tiles, whichever gives the busiest CU fewer rows (ties to the
+// larger tile, which moves less data per MFMA): M=320, N=11008 22.6 us on
+// 64-row tiles (two per CU) against 28.0 us on 128-row tiles (three on some
+// CUs).  A size whose tiles all fit one per CU runs eight waves per tile (two
+// per SIMD: one wave per SIMD leaves its LDS and load waits in series with its
+// MFMAs), else four waves and two workgroups per CU.  Measured, eight against
+// four waves: 64 x 128 at M=64..256, N=K=4096 11.4-11.7 against 12.7 us;
+// 128 x 128 at M=384, N=8192 17.7 against 18.7 us.  The gated epilogue needs
+// two wave columns, so gated 64-row tiles keep four waves.
 template <typename OutT, bool GATED = false>
 int launch_pipe(GemmArgs g, hipStream_t stream) {
   const int64_t cus = cu_count();
   const int64_t tn = (g.N + 127) / 128;
-  const int64_t t256 = ((g.M + 255) / 256) * tn;
+  const int64_t rm256 = (g.M + 255) / 256, rm128 = (g.M + 127) / 128, rm64 = (g.M + 63) / 64;
+  const int64_t t256 = rm256 * tn, t128 = rm128 * tn, t64 = rm64 * tn;
   const int64_t last = t256 % cus;
-  if ((t256 >= cus && (last == 0 || 10 * last > 6 * cus)) || (t256 < cus && 10 * t256 >= 6 * cus))
+  const bool filled =
+      (t256 >= cus && (last == 0 || 10 * last > 6 * cus)) || (t256 < cus && 10 * t256 >= 6 * cus);
+  if (filled && 8 * (rm256 * 256) <= 9 * (rm128 * 128))
     return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1, GATED>(g, stream);
-  if (((g.M + 127) / 128) * tn >= cus)
+  const int64_t busiest128 = (t128 + cus - 1) / cus * 128, busiest64 = (t64 + cus - 1) / cus * 64;
+  if (busiest128 <= busiest64) {
+    if (t128 <= cus) return launch_pipe_cfg<OutT, 128, 128, 4, 2, 2, GATED>(g, stream);
     return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2, GATED>(g, stream);
+  }
   if constexpr (!GATED) {
-    if (((g.M + 63) / 64) * tn <= cus)
-      return launch_pipe_cfg<OutT, 64, 128, 2, 4, 2>(g, stream);
+    if (t64 <= cus) return launch_pipe_cfg<OutT, 64, 128, 2, 4, 2>(g, stream);
   }
   return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2, GATED>(g, stream);
 }

@@ -69,7 +69,7 @@ def _deinterleave(gu_i, N):
 @pytest.mark.parametrize("M,K,N,bias", [(1, 4096, 11008, False), (5, 1088, 640, True),
                                         (16, 4096, 2816, False), (17, 1000, 1024, True),
                                         (64, 4096, 11008, False), (300, 1088, 64, True),
-                                        (512, 4096, 11008, True)])
+                                        (512, 4096, 11008, True), (96, 1088, 11008, True)])
 def test_matmul_silu_mul_matches_unfused_path(gpu, M, K, N, bias):
     """The gated GEMM's h equals the [M, 2N] GEMM + silu_mul_quantize path's h bit
     for bit (the skinny-M kernel for M <= 16, the tiled kernel above; K with a

@@ -14,7 +14,7 @@
 // total every 65536 k.
 //
 // Kernels (dispatch in gemm_typed):
-//   w4a4_gemm_pipe_kernel  the main kernel (M >= 64, or 32 < M < 64 with N >= 8192;
+//   w4a4_gemm_pipe_kernel  the main kernel (M >= 64, or 16 < M < 64 with N > 8064;
 //                          N % 8 == 0): 256-nibble slices, swizzled LDS rows,
 //                          two slices of global loads in flight, one barrier
 //                          per slice (its own comment below);
@@ -881,9 +881,14 @@ bool pipe_layout_ok(const GemmArgs& g) {
          g.brows * KB <= 0xFFFFFFFFll;
 }
 bool pipe_ok(const GemmArgs& g) { return g.M >= 64 && pipe_layout_ok(g); }
-// 32 < M < 64 with N / 128 >= 64 tiles: the pipelined kernel over the skinny-M one.
-bool use_pipe_mid_m(const GemmArgs& g) {
-  return g.M > 32 && g.M < 64 && (g.N + 127) / 128 >= 64 && g.KP <= 65536 && pipe_layout_ok(g);
+// 16 < M < 64 with N / 128 >= 64 tiles: the pipelined kernel over the skinny-M
+// one (its eight-wave 64 x 128 tiles; measured at N=11008, K=4096: M=20..32
+// 10.8-11.0 against 11.8-12.8 us, M=40..56 11.1-11.4 against 17.0-21.2 us; at
+// N <= 4096 the skinny-M kernel stays ahead).  The gated GEMM keeps M > 32: its
+// 64-row tiles run four waves.
+bool use_pipe_mid_m(const GemmArgs& g, bool gated = false) {
+  return g.M > (gated ? 32 : 16) && g.M < 64 && (g.N + 127) / 128 >= 64 && g.KP <= 65536 &&
+         pipe_layout_ok(g);
 }
 
 // DSCQ_GEMM_TILE=<BM>x<BN>[w8] pins the tile shape (tuning sweeps only).
@@ -920,10 +925,10 @@ int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
   if (handled) return rc;
   if (decode || g.M <= 16) return launch_gemv<OutT>(g, stream);
   // 16 < M < 64: the skinny-M kernel streams the weights once per 16 rows but
-  // keeps every CU busy; the pipelined kernel's 64-row tiles pay off once the
-  // skinny kernel needs 3+ passes and N gives 64+ tiles (measured, M = 17..63:
-  // N = K = 4096 skinny 5.5-9.5 us vs pipelined 12.5 us; N = 11008, K = 4096:
-  // skinny 12.1 vs 12.7 us at M = 24, pipelined 12.9 vs 17.1 us at M = 40).
+  // keeps every CU busy; the pipelined kernel's 64-row tiles pay off once N
+  // gives 64+ tiles (measured, M = 20..56: N = K = 4096 skinny 6.3-9.0 us vs
+  // pipelined 10.7-11.3 us; N = 11008, K = 4096 pipelined 10.8-11.4 us vs
+  // skinny 11.8-21.2 us).
   if (g.M < 64) {
     if (use_pipe_mid_m(g)) return launch_pipe<OutT>(g, stream);
     return launch_gemv<OutT>(g, stream);
@@ -998,7 +1003,7 @@ int w4a4_gemm_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
   // Few tokens: the skinny-M kernel streams each weight row once; up to 64
   // rows it keeps doing so unless the pipelined kernel has 64+ tiles (as for
   // dscq_matmul).
-  if (M <= 16 || (M < 64 && !use_pipe_mid_m(g))) return launch_gemv<__half, true>(g, stream);
+  if (M <= 16 || (M < 64 && !use_pipe_mid_m(g, true))) return launch_gemv<__half, true>(g, stream);
   return launch_pipe<__half, true>(g, stream);
 }
 

@@ -70,6 +70,8 @@ MM_CASES = [
     (448, 5120, 512, True, False, False),
     # mid-M with 65 column tiles and a K tail: eight-wave 64 x 128 tiles
     (40, 8200, 320, True, False, False),
+    (24, 8200, 192, False, True, False),
+    (17, 8264, 4096, True, False, False),
     # one round of 128 x 128 tiles (224 of them): eight waves per workgroup
     (192, 14336, 320, True, True, False),
     # 128 x 128 tiles past one round (688), two workgroups per CU

@@ -283,7 +283,7 @@ def main():
         return vendor_int8(args.warm_seconds)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(this build runs the path on a single MI355X)", file=sys.stderr)
+              "(the W4A4 path runs on a single MI355X)", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -504,7 +504,7 @@ def run_graph_steps(args, torch, dev, step):
 def vendor_int8(warm_seconds=2.0):
     """The platform library's dense int8 GEMM (hipBLASLt through torch._int_mm: int8
     operands, int32 result, no int4 unpacking, no epilogue) and fp16 matmul, as a
-    reference point for the W4A4 kernel.  B is K-contiguous (the layout this build's
+    reference point for the W4A4 kernel.  B is K-contiguous (the layout the W4A4
     GEMM reads).  Not part of the default run."""
     import torch
     dev = torch.device("cuda:0")

@@ -104,7 +104,7 @@ def test_matmul_matches_oracle(gpu, M, N, K, use_bias, fp32, force_decode):
     got = out.cpu().numpy()
     np.testing.assert_array_equal(got, out_ref)
     np.testing.assert_array_equal(out_f.cpu().numpy(), got)
-    # north-star tolerance against a float64 dequant of the accumulators
+    # max relative error 1e-3 against a float64 dequant of the accumulators
     exact = _dequant64(raw_ref, sx, zx, sw, sums, bias, M, N)
     rel = np.abs(got.astype(np.float64) - exact) / np.maximum(np.abs(exact), 1e-30)
     big = np.abs(exact) > 1e-2

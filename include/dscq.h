@@ -159,7 +159,8 @@ int dscq_weight_codes(const void* w, int w_dtype, int64_t N, int64_t K,
  *         (the reference's raw-accumulator mode).
  *   force_decode  selects the skinny-M kernel (the reference's decode_gemm,
  *         dispatched there for M < 8) regardless of M; it is also chosen for
- *         M <= 16.  Results are identical either way.
+ *         M <= 16, and for M < 64 unless N > 8064 (64+ column tiles of 128).
+ *         Results are identical either way.
  *   out_fp32  0: out is fp16 [M, N]; 1: fp32.
  * Limits (w4a4.cu:197): 1 <= M <= 65535, N >= 1.
  */

@@ -14,11 +14,13 @@
 // total every 65536 k.
 //
 // Kernels (dispatch in gemm_typed):
-//   w4a4_gemm_pipe_kernel  the main kernel (M >= 64, or 16 < M < 64 with N > 8064;
+//   w4a4_gemm_pipe_kernel  the main kernel (M >= 64 bar the skinny rule below, or
+//                          16 < M < 64 with N > 8064;
 //                          N % 8 == 0): 256-nibble slices, swizzled LDS rows,
 //                          two slices of global loads in flight, one barrier
 //                          per slice (its own comment below);
-//   w4a4_gemv_kernel       M < 64 otherwise, or force_decode: weights streamed
+//   w4a4_gemv_kernel       M < 64 otherwise, ceil(M/16) * N <= 16384 with
+//                          4096 <= KP <= 65536, or force_decode: weights streamed
 //                          once per 16 rows, K split over the waves of a
 //                          workgroup;
 //   w4a4_gemm_kernel       everything else (N % 8 != 0, output not 16-byte
@@ -933,6 +935,15 @@ int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
     if (use_pipe_mid_m(g)) return launch_pipe<OutT>(g, stream);
     return launch_gemv<OutT>(g, stream);
   }
+  // M >= 64 with few weight rows: the pipelined kernel's single round of tiles
+  // takes its serial K loop (~11 us at K = 4096) whatever the size, while the
+  // skinny-M kernel streams the weights once per 16 rows over every CU, so it
+  // stays ahead while ceil(M/16) * N is small (measured at K = 4096: N = 1024,
+  // M = 64..160 6.1-7.5 us against 11.1 us; N = 2048, M = 64..96 6.3-7.5 us
+  // against 11.3 us; N = 4096, M = 64 9.3 against 11.4 us, M = 96 13.0 against
+  // 11.2 us).  Shorter rows keep the pipelined kernel (not measured there).
+  if (g.KP >= 4096 && g.KP <= 65536 && (g.M + 15) / 16 * g.N <= 16384)
+    return launch_gemv<OutT>(g, stream);
   if (g.KP > 65536) return launch_cfg<OutT, 64, 64, 2, 2, true>(g, stream);
   if (pipe_ok(g)) return launch_pipe<OutT>(g, stream);
   const int64_t big_tiles = ((g.M + 127) / 128) * ((g.N + 255) / 256);

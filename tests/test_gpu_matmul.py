@@ -76,6 +76,9 @@ MM_CASES = [
     (192, 14336, 320, True, True, False),
     # 128 x 128 tiles past one round (688), two workgroups per CU
     (512, 22016, 64, False, False, False),
+    # M >= 64 with few weight rows: the skinny-M kernel (ceil(M/16) * N <= 16384)
+    (100, 1000, 4096, True, True, False),
+    (144, 1024, 4160, False, False, False),
 ]
 
 

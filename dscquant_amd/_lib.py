@@ -32,6 +32,9 @@ SIGNATURES = {
     "dscq_pack_weight": [_P, _I, _I64, _I64, _F, _I, _P, _P, _P, _P, _P],
     "dscq_weight_codes": [_P, _I, _I64, _I64, _F, _I, _I, _P, _P, _P],
     "dscq_matmul": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P, _P],
+    "dscq_matmul_ws": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P,
+                       _P, _I64, _P],
+    "dscq_matmul_workspace_bytes": [_I64, _I64, _I64, _I],
     "dscq_linear_decode": [_P, _I, _I64, _I64, _F, _I, _P, _P, _P, _P, _I64, _I, _P, _P],
     "dscq_linear_decode_supported": [_I64, _I64],
     "dscq_pack_int4": [_P, _I64, _I64, _P, _P],
@@ -60,6 +63,7 @@ def lib() -> ctypes.CDLL:
                 fn.restype = ctypes.c_int
             L.dscq_last_error.restype = ctypes.c_char_p
             L.dscq_version.restype = ctypes.c_char_p
+            L.dscq_matmul_workspace_bytes.restype = ctypes.c_int64
             _lib = L
     return _lib
 

@@ -26,7 +26,8 @@ int unpack_int4(const uint8_t* packed, int64_t R, int64_t CB, int64_t width,
 int w4a4_gemm(const uint8_t* a, const uint8_t* b, const float* sx, const int32_t* zx,
               const float* sw, const int32_t* sums, const void* bias, int64_t M,
               int64_t N, int64_t KP, bool decode, bool out_fp32, void* out,
-              int32_t* raw, hipStream_t stream);
+              int32_t* raw, hipStream_t stream, int32_t* ws = nullptr, int64_t ws_bytes = 0);
+int64_t w4a4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t KP, bool decode);
 bool gemm_silu_mul_fits(int64_t M, int64_t NH, int64_t KP, const void* h);
 int w4a4_gemm_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
                        const int32_t* zx, const float* sw, const int32_t* sums,
@@ -220,6 +221,30 @@ int dscq_matmul(const uint8_t* a, const uint8_t* b, const float* sx, const int32
   const bool decode = force_decode != 0 || M < 8;
   return w4a4_gemm(a, b, sx, zx, sw, sums, bias, M, N, KP, decode, out_fp32 != 0, out,
                    fused ? nullptr : raw, static_cast<hipStream_t>(stream));
+}
+
+int64_t dscq_matmul_workspace_bytes(int64_t M, int64_t N, int64_t KP, int force_decode) {
+  if (!(M > 0 && M <= 65535 && N > 0 && N <= 0x7FFFFFFFLL && KP > 0 && KP <= 1048576 &&
+        KP % 64 == 0))
+    return fail("Invalid dimensions");
+  return w4a4_gemm_workspace_bytes(M, N, KP, force_decode != 0 || M < 8);
+}
+
+int dscq_matmul_ws(const uint8_t* a, const uint8_t* b, const float* sx, const int32_t* zx,
+                   const float* sw, const int32_t* sums, const void* bias, int64_t M,
+                   int64_t N, int64_t KP, int fused, int force_decode, int out_fp32,
+                   void* out, int32_t* raw, void* workspace, int64_t workspace_bytes,
+                   void* stream) {
+  if (!(M > 0 && M <= 65535 && N > 0 && KP > 0 && KP <= 1048576 && KP % 64 == 0))
+    return fail("Invalid dimensions");
+  if (N > 0x7FFFFFFFLL) return fail("Invalid dimensions");
+  if (!a || !b || !sx || !zx || !sw || !sums || !out) return fail("matmul: null buffer");
+  if (!fused && !raw) return fail("matmul: the unfused path needs a raw buffer");
+  if (workspace_bytes < 0) return fail("matmul: negative workspace size");
+  const bool decode = force_decode != 0 || M < 8;
+  return w4a4_gemm(a, b, sx, zx, sw, sums, bias, M, N, KP, decode, out_fp32 != 0, out,
+                   fused ? nullptr : raw, static_cast<hipStream_t>(stream),
+                   static_cast<int32_t*>(workspace), workspace_bytes);
 }
 
 int dscq_pack_int4(const int8_t* codes, int64_t R, int64_t C, uint8_t* packed,

@@ -38,6 +38,7 @@
 // for slice k+1 are in flight while slice k feeds the matrix cores; one
 // barrier per slice.
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -63,6 +64,13 @@ struct GemmArgs {
   int64_t M, N, KP;
   int64_t arows, brows;  // readable rows of a (>= MP) and b (>= NP)
   int tiles_n;
+  // K split over workgroups (pipelined kernel only): part p of every tile
+  // covers 256-nibble slices [p * kslices, (p + 1) * kslices) and writes its
+  // int32 sums to part + p * M * N; a second pass adds the parts and applies
+  // the epilogue.
+  int32_t* part = nullptr;
+  int kslices = 0;
+  int tiles = 0;  // tiles per part
 };
 
 constexpr int kSliceBytes = 64;  // 128 nibbles of K per LDS stage
@@ -287,7 +295,7 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 template <typename OutT, int BM, int BN, int WM, int WN, int MINB, bool KTAIL, bool BIAS,
-          bool GATED = false>
+          bool GATED = false, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(GemmArgs g) {
   constexpr int THREADS = 64 * WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32, NF = FM + FN;
@@ -308,12 +316,22 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const int tile_m = blockIdx.x / g.tiles_n;
-  const int tile_n = blockIdx.x % g.tiles_n;
+  int bid = blockIdx.x;
+  int s0 = 0;  // first slice of this workgroup's part of K
+  int32_t* part = nullptr;
+  if constexpr (SPLIT) {
+    const int p = bid / g.tiles;
+    bid -= p * g.tiles;
+    s0 = p * g.kslices;
+    part = g.part + (int64_t)p * g.M * g.N;
+  }
+  const int tile_m = bid / g.tiles_n;
+  const int tile_n = bid % g.tiles_n;
   const int64_t m0 = (int64_t)tile_m * BM;
   const int64_t n0 = (int64_t)tile_n * BN;
   const int64_t KB = g.KP / 2;
-  const int nslices = (int)((KB + SB - 1) / SB);
+  const int nslices = SPLIT ? min(g.kslices, (int)((KB + SB - 1) / SB) - s0)
+                            : (int)((KB + SB - 1) / SB);
 
   // Global pieces of this thread: unit u = tid % UNITS of rows
   // tid / UNITS + (THREADS / UNITS) i -- rows of A for i < BM / (THREADS / UNITS),
@@ -335,7 +353,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   const int wr_off = (tid / UNITS) * SB + 16 * (u ^ ((tid / UNITS >> 1) & 7));
 
   auto gload = [&](uint4 (&st)[LOADS], int slice) {
-    const int sl = min(slice, nslices - 1);
+    const int sl = s0 + min(slice, nslices - 1);
     int64_t kb = (int64_t)sl * SB;
     // Pieces past the row end (only in the last slice when KB % SB != 0) read
     // the row's last in-bounds piece and are zeroed.
@@ -510,6 +528,23 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   // the K loop.
   const int rl = lane & 31;
   const int cq = 4 * (lane >> 5);
+  if constexpr (SPLIT) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int64_t row = m0 + wm * TM + i * 32 + rl;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t c0 = n0 + wn * TN + j * 32 + 8 * q + cq;
+          if (row < g.M && c0 < g.N)
+            *reinterpret_cast<int4*>(part + row * g.N + c0) =
+                make_int4(acc[i][j][4 * q] >> 8, acc[i][j][4 * q + 1] >> 8,
+                          acc[i][j][4 * q + 2] >> 8, acc[i][j][4 * q + 3] >> 8);
+        }
+    }
+    return;
+  }
   float sxr[FM];
   int32_t zr[FM];
 #pragma unroll
@@ -714,6 +749,114 @@ int launch_pipe(GemmArgs g, hipStream_t stream) {
     if (t64 <= cus) return launch_pipe_cfg<OutT, 64, 128, 2, 4, 2>(g, stream);
   }
   return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2, GATED>(g, stream);
+}
+
+// Second pass of a K split: adds the int32 parts of four adjacent outputs
+// (exact in any order) and applies the epilogue in the pipelined kernel's
+// operation order.  N % 8 == 0, so the four columns share a row.
+template <typename OutT, bool BIAS>
+__global__ __launch_bounds__(256) void w4a4_split_reduce_kernel(GemmArgs g, int parts) {
+  const int64_t total = g.M * g.N;
+  const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (idx >= total) return;
+  const int64_t row = idx / g.N, col = idx - row * g.N;
+  int4 r = *reinterpret_cast<const int4*>(g.part + idx);
+  for (int p = 1; p < parts; ++p) {
+    const int4 v = *reinterpret_cast<const int4*>(g.part + p * total + idx);
+    r.x += v.x;
+    r.y += v.y;
+    r.z += v.z;
+    r.w += v.w;
+  }
+  const int32_t z = 8 - g.zx[row];
+  const float sx = g.sx[row];
+  const int32_t rv[4] = {r.x, r.y, r.z, r.w};
+  float res[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int32_t corrected = rv[c] + __mul24(z, g.sums[col + c]);
+    float v = (float)corrected * sx;
+    v = v * g.sw[col + c];
+    if (BIAS) v = v + (float)static_cast<const OutT*>(g.bias)[col + c];
+    res[c] = v;
+  }
+  OutT* out = static_cast<OutT*>(g.out);
+  if constexpr (sizeof(OutT) == 2) {
+    uint2 pk;
+    pk.x = (uint32_t)__half_as_ushort(to_out<__half>(res[0])) |
+           ((uint32_t)__half_as_ushort(to_out<__half>(res[1])) << 16);
+    pk.y = (uint32_t)__half_as_ushort(to_out<__half>(res[2])) |
+           ((uint32_t)__half_as_ushort(to_out<__half>(res[3])) << 16);
+    *reinterpret_cast<uint2*>(out + idx) = pk;
+  } else {
+    *reinterpret_cast<float4*>(out + idx) = make_float4(res[0], res[1], res[2], res[3]);
+  }
+  if (g.raw) *reinterpret_cast<int4*>(g.raw + idx) = r;
+}
+
+// K split for the 64 x 128 eight-wave pick when its tiles leave most CUs idle
+// and K is long (small-batch down projections): one workgroup per CU, parts of
+// at least eight slices, at most eight parts, and at least twelve slices saved
+// per workgroup so that the saving outweighs the second pass (~2-5 us).
+// Measured: M=128, N=4096, K=11008 25.0 -> 19.0 us; where the tiles already
+// fill the CUs or K is short, splitting is slower (M=512, N=4096, K=11008
+// 29.6 -> 34.3 us with two workgroups per CU; M=256, K=N=4096 12.3 -> 18.8 us).
+// 0 when not split.
+int split_parts(const GemmArgs& g) {
+  const int64_t cus = cu_count();
+  const int64_t tn = (g.N + 127) / 128;
+  const int64_t t64 = ((g.M + 63) / 64) * tn, t128 = ((g.M + 127) / 128) * tn;
+  const int64_t busiest128 = (t128 + cus - 1) / cus * 128, busiest64 = (t64 + cus - 1) / cus * 64;
+  if (t64 > cus || busiest128 <= busiest64) return 0;
+  const int64_t nsl = (g.KP / 2 + 127) / 128;
+  const int64_t parts = std::min<int64_t>(std::min<int64_t>(cus / t64, nsl / 8), 8);
+  if (parts < 2) return 0;
+  const int64_t ks = (nsl + parts - 1) / parts;
+  if (nsl - ks < 12) return 0;
+  return (int)((nsl + ks - 1) / ks);  // every part non-empty
+}
+
+template <typename OutT>
+int launch_pipe_split(GemmArgs g, int parts, int32_t* ws, hipStream_t stream) {
+  g.tiles_n = (int)((g.N + 127) / 128);
+  g.tiles = (int)(((g.M + 63) / 64) * g.tiles_n);
+  const int64_t nsl = (g.KP / 2 + 127) / 128;
+  g.kslices = (int)((nsl + parts - 1) / parts);
+  g.part = ws;
+  const int64_t quads = g.M * g.N / 4;
+  if ((quads + 255) / 256 > 0x7FFFFFFF) return fail("matmul: grid too large");
+  const bool ktail = (g.KP / 2) % 128 != 0;
+  const dim3 grid((unsigned)(g.tiles * parts)), block(512);
+  if (ktail)
+    hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<OutT, 64, 128, 2, 4, 2, true, false, false, true>),
+                       grid, block, 0, stream, g);
+  else
+    hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<OutT, 64, 128, 2, 4, 2, false, false, false, true>),
+                       grid, block, 0, stream, g);
+  const int rc = launch_status("w4a4_gemm_pipe_kernel");
+  if (rc) return rc;
+  const dim3 rgrid((unsigned)((quads + 255) / 256)), rblock(256);
+  if (g.bias)
+    hipLaunchKernelGGL((w4a4_split_reduce_kernel<OutT, true>), rgrid, rblock, 0, stream, g, parts);
+  else
+    hipLaunchKernelGGL((w4a4_split_reduce_kernel<OutT, false>), rgrid, rblock, 0, stream, g, parts);
+  return launch_status("w4a4_split_reduce_kernel");
+}
+
+int64_t split_workspace_bytes(const GemmArgs& g) {
+  const int parts = split_parts(g);
+  return parts >= 2 ? (int64_t)parts * g.M * g.N * 4 : 0;
+}
+
+// The pipelined kernel, split over K when a workspace (16-byte aligned, large
+// enough) was given and the shape asks for it.
+template <typename OutT>
+int launch_pipe_ws(const GemmArgs& g, int32_t* ws, int64_t ws_bytes, hipStream_t stream) {
+  if (ws && (reinterpret_cast<uintptr_t>(ws) & 15) == 0) {
+    const int64_t need = split_workspace_bytes(g);
+    if (need > 0 && ws_bytes >= need) return launch_pipe_split<OutT>(g, split_parts(g), ws, stream);
+  }
+  return launch_pipe<OutT>(g, stream);
 }
 
 template <typename OutT, int BM, int BN, int WM, int WN, bool HUGE>
@@ -921,7 +1064,8 @@ int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
 }
 
 template <typename OutT>
-int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
+int gemm_typed(const GemmArgs& g, bool decode, int32_t* ws, int64_t ws_bytes,
+               hipStream_t stream) {
   int handled = 0;
   const int rc = tile_override<OutT>(g, stream, &handled);
   if (handled) return rc;
@@ -932,7 +1076,7 @@ int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
   // pipelined 10.7-11.3 us; N = 11008, K = 4096 pipelined 10.8-11.4 us vs
   // skinny 11.8-21.2 us).
   if (g.M < 64) {
-    if (use_pipe_mid_m(g)) return launch_pipe<OutT>(g, stream);
+    if (use_pipe_mid_m(g)) return launch_pipe_ws<OutT>(g, ws, ws_bytes, stream);
     return launch_gemv<OutT>(g, stream);
   }
   // M >= 64 with few weight rows: the pipelined kernel's single round of tiles
@@ -945,18 +1089,44 @@ int gemm_typed(const GemmArgs& g, bool decode, hipStream_t stream) {
   if (g.KP >= 4096 && g.KP <= 65536 && (g.M + 15) / 16 * g.N <= 16384)
     return launch_gemv<OutT>(g, stream);
   if (g.KP > 65536) return launch_cfg<OutT, 64, 64, 2, 2, true>(g, stream);
-  if (pipe_ok(g)) return launch_pipe<OutT>(g, stream);
+  if (pipe_ok(g)) return launch_pipe_ws<OutT>(g, ws, ws_bytes, stream);
   const int64_t big_tiles = ((g.M + 127) / 128) * ((g.N + 255) / 256);
   if (big_tiles >= 192) return launch_cfg<OutT, 128, 256, 2, 2, false>(g, stream);
   return launch_cfg<OutT, 128, 128, 2, 2, false>(g, stream);
 }
 
+// Whether gemm_typed takes the pipelined kernel (tuning overrides aside).
+bool takes_pipe(const GemmArgs& g, bool decode) {
+  if (decode || g.M <= 16) return false;
+  if (g.M < 64) return use_pipe_mid_m(g);
+  if (g.KP >= 4096 && g.KP <= 65536 && (g.M + 15) / 16 * g.N <= 16384) return false;
+  if (g.KP > 65536) return false;
+  return pipe_ok(g);
+}
+
 }  // namespace
+
+int64_t w4a4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t KP, bool decode) {
+  GemmArgs g;
+  g.a = g.b = nullptr;
+  g.sx = g.sw = nullptr;
+  g.zx = g.sums = nullptr;
+  g.bias = nullptr;
+  g.out = nullptr;
+  g.raw = nullptr;
+  g.M = M;
+  g.N = N;
+  g.KP = KP;
+  g.arows = ceil_to(M, 8);
+  g.brows = ceil_to(N, 8);
+  g.tiles_n = 0;
+  return takes_pipe(g, decode) ? split_workspace_bytes(g) : 0;
+}
 
 int w4a4_gemm(const uint8_t* a, const uint8_t* b, const float* sx, const int32_t* zx,
               const float* sw, const int32_t* sums, const void* bias, int64_t M,
               int64_t N, int64_t KP, bool decode, bool out_fp32, void* out,
-              int32_t* raw, hipStream_t stream) {
+              int32_t* raw, hipStream_t stream, int32_t* ws, int64_t ws_bytes) {
   GemmArgs g;
   g.a = a;
   g.b = b;
@@ -973,8 +1143,8 @@ int w4a4_gemm(const uint8_t* a, const uint8_t* b, const float* sx, const int32_t
   g.arows = ceil_to(M, 8);
   g.brows = ceil_to(N, 8);
   g.tiles_n = 0;
-  return out_fp32 ? gemm_typed<float>(g, decode, stream)
-                  : gemm_typed<__half>(g, decode, stream);
+  return out_fp32 ? gemm_typed<float>(g, decode, ws, ws_bytes, stream)
+                  : gemm_typed<__half>(g, decode, ws, ws_bytes, stream);
 }
 
 // The gated GEMM's shape requirements (the caller reports them): h columns a

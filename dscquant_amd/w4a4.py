@@ -27,7 +27,7 @@ from . import _lib
 
 __all__ = ["quantize", "matmul", "pack_weight", "silu_mul_quantize", "linear_decode",
            "linear_decode_supported", "matmul_silu_mul", "interleave_gate_up", "padded",
-           "check_quantize_args", "check_matmul_args"]
+           "check_quantize_args", "check_matmul_args", "workspace_bytes"]
 
 
 def padded(v: int, m: int) -> int:
@@ -129,12 +129,25 @@ def matmul(a, b, sx, zx, sw, sums, bias, M: int, N: int, fused: bool = True,
     _lib.require_gfx950(dev)
     out = torch.empty((M, N), dtype=torch.float32 if fp32 else torch.float16, device=dev)
     raw = torch.empty((0,) if fused else (M, N), dtype=torch.int32, device=dev)
+    # Shapes whose K loop the library splits over workgroups take a scratch
+    # workspace, allocated here like the outputs (dscq_matmul_ws).
+    ws_bytes = workspace_bytes(M, N, KP, force_decode)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev) if ws_bytes else None
     with torch.cuda.device(dev):
-        _lib.call("dscq_matmul", a.data_ptr(), b.data_ptr(), sx.data_ptr(), zx.data_ptr(),
+        _lib.call("dscq_matmul_ws", a.data_ptr(), b.data_ptr(), sx.data_ptr(), zx.data_ptr(),
                   sw.data_ptr(), sums.data_ptr(), _lib.ptr(bias), M, N, KP,
                   1 if fused else 0, 1 if force_decode else 0, 1 if fp32 else 0,
-                  out.data_ptr(), _lib.ptr(raw), _lib.stream(dev))
+                  out.data_ptr(), _lib.ptr(raw), _lib.ptr(ws), ws_bytes, _lib.stream(dev))
     return [out, raw]
+
+
+def workspace_bytes(M: int, N: int, KP: int, force_decode: bool = False) -> int:
+    """Scratch bytes ``matmul`` passes to dscq_matmul_ws for this shape (0: none)."""
+    n = int(_lib.lib().dscq_matmul_workspace_bytes(int(M), int(N), int(KP),
+                                                   1 if force_decode else 0))
+    if n < 0:
+        raise RuntimeError(_lib.lib().dscq_last_error().decode())
+    return n
 
 
 def linear_decode_supported(M: int, K: int) -> bool:

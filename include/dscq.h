@@ -170,6 +170,29 @@ int dscq_matmul(const uint8_t* a, const uint8_t* b, const float* sx,
                 int force_decode, int out_fp32, void* out, int32_t* raw,
                 void* stream);
 
+/* dscq_matmul with a caller-provided device workspace (no counterpart in the
+ * reference, whose matmul, kernel/w4a4.cu:189-225, allocates only its
+ * outputs; the Python matmul allocates the workspace the same way, from
+ * torch's allocator).  Shapes for which one round of 64 x 128 tiles leaves the
+ * K loop's latency exposed (small M with few output tiles, long K) then split
+ * K over workgroups: int32 partial sums per part go to the workspace and a
+ * second kernel adds them and applies the epilogue.  Integer partial sums add
+ * exactly, so the results are bit-identical to dscq_matmul's.
+ *   workspace        NULL, or 16-byte aligned device memory of
+ *                    workspace_bytes; too small, misaligned or NULL: no split.
+ * Every other argument and error is as for dscq_matmul.  The workspace is
+ * scratch for this call only; calls that may overlap need their own. */
+int dscq_matmul_ws(const uint8_t* a, const uint8_t* b, const float* sx,
+                   const int32_t* zx, const float* sw, const int32_t* sums,
+                   const void* bias, int64_t M, int64_t N, int64_t KP, int fused,
+                   int force_decode, int out_fp32, void* out, int32_t* raw,
+                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of workspace dscq_matmul_ws uses for this shape (0: it does not split;
+ * the workspace may then be NULL), or a negative value for invalid dimensions
+ * (as dscq_matmul reports them).  Host-only: launches nothing. */
+int64_t dscq_matmul_workspace_bytes(int64_t M, int64_t N, int64_t KP, int force_decode);
+
 /*
  * Standalone int4 packer for signed codes already in [-8, 7]: the GPU form
  * of pack_int4 (core/quantization.py:31-40; range checking is the caller's,

@@ -82,6 +82,27 @@ def test_c_matmul_argument_checks():
                                    None, None)
 
 
+def test_c_matmul_ws_argument_checks_and_workspace_query():
+    d = 16
+    for M, N, KP in ((0, 8, 64), (65536, 8, 64), (4, 8, 96)):
+        assert _einval("dscq_matmul_ws", d, d, d, d, d, d, None, M, N, KP, 1, 0, 0, d, None,
+                       None, 0, None) == "Invalid dimensions"
+        assert _lib.lib().dscq_matmul_workspace_bytes(M, N, KP, 0) < 0
+    assert "workspace" in _einval("dscq_matmul_ws", d, d, d, d, d, d, None, 4, 8, 64, 1, 0, 0,
+                                  d, None, None, -1, None)
+    q = _lib.lib().dscq_matmul_workspace_bytes
+    # host-only: few 64 x 128 tiles with a long K split into int32 parts of
+    # [M, N] (256 compute units assumed where no device is visible)
+    assert q(128, 4096, 11008, 0) == 4 * 128 * 4096 * 4
+    assert q(512, 4096, 11008, 0) == 0      # the tiles already fill the CUs
+    assert q(128, 4096, 4096, 0) == 0       # K too short to pay for the second pass
+    assert q(2048, 4096, 4096, 0) == 0      # full rounds of 256 x 128 tiles
+    assert q(8, 4096, 4096, 0) == 0         # skinny-M kernel
+    assert q(128, 4096, 4096, 1) == 0       # forced decode
+    assert q(512, 4100, 11008, 0) == 0      # N % 8 != 0: general kernel
+    assert w4a4.workspace_bytes(128, 4096, 11008) == 4 * 128 * 4096 * 4
+
+
 def test_c_other_argument_checks():
     d = 16
     assert "bits" in _einval("dscq_activation_codes", d, 0, 4, 64, 1.0, 9, 0, d, d, d, None)

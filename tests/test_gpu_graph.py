@@ -43,7 +43,7 @@ def _replay_and_compare(fn, inputs):
             assert torch.equal(o, r), f"replay {rep} differs from eager"
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 4096, 1024), (16, 4096, 4096)])
+@pytest.mark.parametrize("M,K,N", [(256, 4096, 1024), (16, 4096, 4096), (128, 11008, 4096)])
 def test_quantize_matmul_graph(gpu, M, K, N):
     print(f"graph quantize+matmul M{M} K{K} N{N}", flush=True)
     pw, sw, sums = w4a4.pack_weight(torch.from_numpy(weights(N, K, seed=9)).to(gpu), 1.0, 128)

@@ -79,6 +79,9 @@ MM_CASES = [
     # M >= 64 with few weight rows: the skinny-M kernel (ceil(M/16) * N <= 16384)
     (100, 1000, 4096, True, True, False),
     (144, 1024, 4160, False, False, False),
+    # K split over workgroups (few 64 x 128 tiles, long K): 4 and 5 parts
+    (130, 2056, 8384, True, True, False),
+    (64, 4104, 11072, False, False, False),
 ]
 
 

@@ -48,6 +48,9 @@ WORKLOADS = {
     "70b_qo": (4096, 8192, 8192, 128),
     "70b_up": (4096, 28672, 8192, 128),
     "70b_down": (4096, 8192, 28672, 128),
+    # small-batch MLP down projection (128 tokens): few 64x128 tiles over a
+    # long K, split over workgroups through dscq_matmul_ws
+    "down_b128": (128, 4096, 11008, 128),
     # SiLU-gated MLP block (Llama-7B shapes): x[M,K] -> gate|up GEMM [M, 2N] ->
     # silu*up + rotate + quantize -> down GEMM [M, K]
     "mlp": (512, 11008, 4096, 128),
@@ -320,10 +323,16 @@ def main():
                              sx.data_ptr(), zx.data_ptr(), None, _lib.stream(dev))
         assert rc == 0, L.dscq_last_error()
 
+    # scratch for the K split (0 bytes unless few tiles meet a long K), allocated
+    # once, outside the timed region, as a caller of dscq_matmul_ws would
+    nws = L.dscq_matmul_workspace_bytes(M, N, KP, 0)
+    assert nws >= 0, L.dscq_last_error()
+    ws = torch.empty((max(nws, 16),), dtype=torch.uint8, device=dev)
+
     def gemm():
-        rc = L.dscq_matmul(pa.data_ptr(), packed_w.data_ptr(), sx.data_ptr(), zx.data_ptr(),
-                           sw.data_ptr(), sums.data_ptr(), None, M, N, KP, 1, 0, 0,
-                           out.data_ptr(), None, _lib.stream(dev))
+        rc = L.dscq_matmul_ws(pa.data_ptr(), packed_w.data_ptr(), sx.data_ptr(), zx.data_ptr(),
+                              sw.data_ptr(), sums.data_ptr(), None, M, N, KP, 1, 0, 0,
+                              out.data_ptr(), None, ws.data_ptr(), nws, _lib.stream(dev))
         assert rc == 0, L.dscq_last_error()
 
     def step(i):

@@ -129,11 +129,12 @@ def matmul(a, b, sx, zx, sw, sums, bias, M: int, N: int, fused: bool = True,
     _lib.require_gfx950(dev)
     out = torch.empty((M, N), dtype=torch.float32 if fp32 else torch.float16, device=dev)
     raw = torch.empty((0,) if fused else (M, N), dtype=torch.int32, device=dev)
-    # Shapes whose K loop the library splits over workgroups take a scratch
-    # workspace, allocated here like the outputs (dscq_matmul_ws).
-    ws_bytes = workspace_bytes(M, N, KP, force_decode)
-    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev) if ws_bytes else None
     with torch.cuda.device(dev):
+        # Shapes whose K loop the library splits over workgroups take a scratch
+        # workspace, allocated here like the outputs (dscq_matmul_ws); the size
+        # depends on the device's compute units, so it is asked on that device.
+        ws_bytes = workspace_bytes(M, N, KP, force_decode)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev) if ws_bytes else None
         _lib.call("dscq_matmul_ws", a.data_ptr(), b.data_ptr(), sx.data_ptr(), zx.data_ptr(),
                   sw.data_ptr(), sums.data_ptr(), _lib.ptr(bias), M, N, KP,
                   1 if fused else 0, 1 if force_decode else 0, 1 if fp32 else 0,

@@ -132,27 +132,36 @@ def time_kernel(launch, n, torch, dev):
 
 
 def time_in_steps(kernels, n, torch, lead=512):
-    """Average device time of each kernel of a step, measured inside n eager
-    steps with HIP events on the launch stream between consecutive kernels.
-    The kernels run in the mix the timed steps run them in (a GEMM right after
-    a quantize kernel) rather than a hundred launches of one kernel back to
-    back, whose sustained power draw lowers the clock; a kernel trace of the
-    bench command averages the same mix."""
+    """Average device duration of each kernel of a step, over n eager steps that
+    run the kernels in the mix the timed steps run them in (a GEMM right after a
+    quantize kernel) rather than a hundred launches of one kernel back to back,
+    whose sustained power draw lowers the clock.  Each launch stamps its own
+    start and end into a pair of HIP events on its stream (dscq_time_next_kernel:
+    hipExtLaunchKernel), so the figure is the kernel's duration as a kernel trace
+    reports it, without the event markers and dispatch gaps that events recorded
+    around a call would add (~2 us per interval on this platform)."""
+    from dscquant_amd import _lib
+    L = _lib.lib()
     nk = len(kernels)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(nk + 1)] for _ in range(n)]
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(nk)] for _ in range(n)]
+    for row in evs:  # torch creates the HIP events on their first record
+        for start, end in row:
+            start.record()
+            end.record()
     torch.cuda.synchronize()
     # A lead of untimed steps keeps the GPU busy while the host queues the timed
-    # ones, so no interval between two events waits for the host.
+    # ones, as in the graph-replayed steps.
     for i in range(lead):
         for fn in kernels:
             fn(i)
     for i in range(n):
         for k, fn in enumerate(kernels):
-            evs[i][k].record()
+            start, end = evs[i][k]
+            L.dscq_time_next_kernel(start.cuda_event, end.cuda_event)
             fn(i)
-        evs[i][nk].record()
     torch.cuda.synchronize()
-    return [sum(evs[i][k].elapsed_time(evs[i][k + 1]) for i in range(n)) / n * 1e-3
+    return [sum(evs[i][k][0].elapsed_time(evs[i][k][1]) for i in range(n)) / n * 1e-3
             for k in range(nk)]
 
 
@@ -239,13 +248,32 @@ def cpu_model():
     return "unknown"
 
 
+def cpu_threads():
+    """Threads for the CPU baseline: every core this process may use.  A GPU
+    box's share of its host is set by OMP_NUM_THREADS and the CPU affinity
+    mask, which can be fewer than os.cpu_count() reports for the whole host."""
+    host = os.cpu_count() or 1
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = host
+    limit = allowed
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        limit = min(limit, int(env))
+    share = (f"all {host} host cores" if limit == host else
+             f"this process's share: {limit} of {host} host cores "
+             f"(affinity {allowed}, OMP_NUM_THREADS={env or 'unset'})")
+    return limit, share
+
+
 def cpu_baseline(M, N, K, budget_s):
     """The reference's CPU fake-quant forward on the same workload, median time:
     as the reference runs it (weight re-quantized on every call) and with the
     fake-quantized weight cached, each on half of the time budget."""
     import torch
     from oracle import fakequant
-    threads = min(16, os.cpu_count() or 1)
+    threads, share = cpu_threads()
     torch.set_num_threads(threads)
     x, w = synthetic(M, N, K)
 
@@ -271,7 +299,7 @@ def cpu_baseline(M, N, K, budget_s):
         "sample": (f"torch-CPU fake-quant QuantLinear.forward (core/linear.py:48-52), "
                    f"weights re-quantized per call, M={M} N={N} K={K} fp16, "
                    f"median of {n} runs ({med * 1e3:.1f} ms/run) on {threads} threads of "
-                   f"{cpu_model()}"),
+                   f"{cpu_model()} ({share})"),
         "weights_cached": {"value": round(ops / med_c / 1e12, 4), "unit": "TOPS",
                            "ms_per_run": round(med_c * 1e3, 2), "runs": n_c},
     }
@@ -603,20 +631,22 @@ def main_decode(args, torch, _lib, w4a4):
 
     warm_up(step, args.warm_seconds, torch)
     t_two = time_kernel(two_launch, args.kernel_iters, torch, dev)
-    t_quant = time_kernel(quantize, args.kernel_iters, torch, dev)
-    quantize(0)
-    t_gemv = time_kernel(gemv, args.kernel_iters, torch, dev)
-    t_fused = time_kernel(fused, args.kernel_iters, torch, dev) if fused_ok else None
+    t_quant, t_gemv = time_in_steps([quantize, gemv], args.kernel_iters, torch)
+    t_fused = time_in_steps([fused], args.kernel_iters, torch)[0] if fused_ok else None
+    t_fused_iso = time_kernel(fused, args.kernel_iters, torch, dev) if fused_ok else None
     t_step = run_graph_steps(args, torch, dev, step)
     ops = 2.0 * M * N * K
     traffic = load_traffic(args.workload) or {}
 
-    def hbm_line(kernel, dbytes, t, cls):
+    def hbm_line(kernel, dbytes, t, cls, t_iso=None):
         gbs = dbytes / t / 1e9
-        return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+        line = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "kernel": kernel,
                 "avg_us": round(t * 1e6, 3), "bytes_per_launch": dbytes,
                 "traffic": traffic[cls]["traffic"] if cls in traffic else None}
+        if t_iso is not None:
+            line["isolated_us"] = round(t_iso * 1e6, 3)
+        return line
 
     # skinny GEMM: packed weights + packed activations + sw, sums, sx, zx + out (fp16)
     gemv_line = hbm_line("w4a4_gemv_kernel", wbytes + M * KP // 2 + 8 * N + 8 * M + 2 * M * N,
@@ -627,7 +657,7 @@ def main_decode(args, torch, _lib, w4a4):
     if fused_ok:
         # weights + x (fp16) + sw, sums + out (fp16)
         line = hbm_line("w4a4_decode_kernel", wbytes + 2 * M * K + 8 * N + 2 * M * N, t_fused,
-                        "decode")
+                        "decode", t_fused_iso)
         kernels = {"decode_fused": line, **kernels}
         how = "fused quantize + skinny product (one launch)"
     else:

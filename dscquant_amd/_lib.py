@@ -39,6 +39,7 @@ SIGNATURES = {
     "dscq_linear_decode_supported": [_I64, _I64],
     "dscq_pack_int4": [_P, _I64, _I64, _P, _P],
     "dscq_unpack_int4": [_P, _I64, _I64, _I64, _P, _P],
+    "dscq_time_next_kernel": [_P, _P],
     "dscq_device_supported": [],
     "dscq_last_error": [],
     "dscq_version": [],

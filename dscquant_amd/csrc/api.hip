@@ -40,6 +40,13 @@ int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, in
 
 namespace {
 thread_local char g_last_error[512] = "";
+thread_local KernelEvents g_kernel_events = {nullptr, nullptr};
+}  // namespace
+
+KernelEvents take_kernel_events() {
+  const KernelEvents ev = g_kernel_events;
+  g_kernel_events = {nullptr, nullptr};
+  return ev;
 }
 
 int fail(const char* fmt, ...) {
@@ -80,7 +87,12 @@ extern "C" {
 
 const char* dscq_last_error(void) { return g_last_error; }
 
-const char* dscq_version(void) { return "dscq 0.1.0 (gfx950)"; }
+const char* dscq_version(void) { return "dscq 0.2.0 (gfx950)"; }
+
+int dscq_time_next_kernel(void* start, void* stop) {
+  g_kernel_events = {static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
+  return DSCQ_OK;
+}
 
 int dscq_device_supported(void) {
   int dev = 0;

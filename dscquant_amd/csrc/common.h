@@ -1,6 +1,7 @@
 // Shared device helpers and host error plumbing for libdscq (gfx950 only).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -17,6 +18,26 @@ int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 int launch_status(const char* what);
 
 inline int64_t ceil_to(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Events armed by dscq_time_next_kernel for this thread's next kernel launch
+// (both null when none is armed); taking them disarms them.
+struct KernelEvents {
+  hipEvent_t start, stop;
+};
+KernelEvents take_kernel_events();
+
+// Every kernel of the library is launched through here.  With events armed the
+// launch goes through hipExtLaunchKernel, which stamps the kernel's own start
+// and end into them (a kernel trace's duration, without event markers around
+// the launch).
+template <typename F, typename... Args>
+void launch(F kernel, dim3 grid, dim3 block, hipStream_t stream, Args... args) {
+  const KernelEvents ev = take_kernel_events();
+  if (ev.start || ev.stop)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, ev.start, ev.stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+}
 
 // -------------------------------------------------------------- device side
 

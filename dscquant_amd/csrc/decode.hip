@@ -347,11 +347,11 @@ int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, in
   const int64_t iters = (M * d.nblk + 31) / 32;
 #define DSCQ_DEC_I(T, O, R, B, P)                                                              \
   if (iters <= 1)                                                                              \
-    hipLaunchKernelGGL((w4a4_decode_kernel<T, O, R, B, P, 1>), grid, block, 0, stream, d);    \
+    launch((w4a4_decode_kernel<T, O, R, B, P, 1>), grid, block, stream, d);    \
   else if (iters <= 2)                                                                         \
-    hipLaunchKernelGGL((w4a4_decode_kernel<T, O, R, B, P, 2>), grid, block, 0, stream, d);    \
+    launch((w4a4_decode_kernel<T, O, R, B, P, 2>), grid, block, stream, d);    \
   else                                                                                         \
-    hipLaunchKernelGGL((w4a4_decode_kernel<T, O, R, B, P, 0>), grid, block, 0, stream, d);
+    launch((w4a4_decode_kernel<T, O, R, B, P, 0>), grid, block, stream, d);
 #define DSCQ_DEC(T, O, R, B)                                                                   \
   if (per <= 4) {                                                                              \
     DSCQ_DEC_I(T, O, R, B, 4)                                                                  \

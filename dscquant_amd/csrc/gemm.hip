@@ -686,9 +686,8 @@ int launch_pipe_cfg(GemmArgs g, hipStream_t stream) {
   const bool ktail = (g.KP / 2) % 128 != 0;  // rows end inside a 128-byte slice
   const dim3 grid((unsigned)nblocks), block(64 * WM * WN);
 #define DSCQ_PIPE(KT, BI)                                                                  \
-  hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<OutT, BM, BN, WM, WN, MINB, KT, BI, GATED>), grid,   \
-                     block,                                                                    \
-                     0, stream, g)
+  launch((w4a4_gemm_pipe_kernel<OutT, BM, BN, WM, WN, MINB, KT, BI, GATED>), grid, block, \
+         stream, g)
   if (g.bias) {
     if (ktail) DSCQ_PIPE(true, true); else DSCQ_PIPE(false, true);
   } else {
@@ -828,18 +827,18 @@ int launch_pipe_split(GemmArgs g, int parts, int32_t* ws, hipStream_t stream) {
   const bool ktail = (g.KP / 2) % 128 != 0;
   const dim3 grid((unsigned)(g.tiles * parts)), block(512);
   if (ktail)
-    hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<OutT, 64, 128, 2, 4, 2, true, false, false, true>),
-                       grid, block, 0, stream, g);
+    launch((w4a4_gemm_pipe_kernel<OutT, 64, 128, 2, 4, 2, true, false, false, true>),
+                       grid, block, stream, g);
   else
-    hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<OutT, 64, 128, 2, 4, 2, false, false, false, true>),
-                       grid, block, 0, stream, g);
+    launch((w4a4_gemm_pipe_kernel<OutT, 64, 128, 2, 4, 2, false, false, false, true>),
+                       grid, block, stream, g);
   const int rc = launch_status("w4a4_gemm_pipe_kernel");
   if (rc) return rc;
   const dim3 rgrid((unsigned)((quads + 255) / 256)), rblock(256);
   if (g.bias)
-    hipLaunchKernelGGL((w4a4_split_reduce_kernel<OutT, true>), rgrid, rblock, 0, stream, g, parts);
+    launch((w4a4_split_reduce_kernel<OutT, true>), rgrid, rblock, stream, g, parts);
   else
-    hipLaunchKernelGGL((w4a4_split_reduce_kernel<OutT, false>), rgrid, rblock, 0, stream, g, parts);
+    launch((w4a4_split_reduce_kernel<OutT, false>), rgrid, rblock, stream, g, parts);
   return launch_status("w4a4_split_reduce_kernel");
 }
 
@@ -866,8 +865,8 @@ int launch_cfg(GemmArgs g, hipStream_t stream) {
   const int64_t nblocks = tiles_m * g.tiles_n;
   if (nblocks > 0x7FFFFFFF) return fail("matmul: grid too large (M=%lld, N=%lld)",
                                         (long long)g.M, (long long)g.N);
-  hipLaunchKernelGGL((w4a4_gemm_kernel<OutT, BM, BN, WM, WN, HUGE>), dim3((unsigned)nblocks),
-                     dim3(64 * WM * WN), 0, stream, g);
+  launch((w4a4_gemm_kernel<OutT, BM, BN, WM, WN, HUGE>), dim3((unsigned)nblocks),
+                     dim3(64 * WM * WN), stream, g);
   return launch_status("w4a4_gemm_kernel");
 }
 
@@ -1011,9 +1010,9 @@ int launch_gemv(GemmArgs g, hipStream_t stream) {
   if (gx > 0x7FFFFFFF || gy > 65535) return fail("matmul: grid too large");
   const dim3 grid((unsigned)gx, (unsigned)gy), block(512);
   if (g.bias)
-    hipLaunchKernelGGL((w4a4_gemv_kernel<OutT, true, GATED>), grid, block, 0, stream, g);
+    launch((w4a4_gemv_kernel<OutT, true, GATED>), grid, block, stream, g);
   else
-    hipLaunchKernelGGL((w4a4_gemv_kernel<OutT, false, GATED>), grid, block, 0, stream, g);
+    launch((w4a4_gemv_kernel<OutT, false, GATED>), grid, block, stream, g);
   return launch_status("w4a4_gemv_kernel");
 }
 
@@ -1036,39 +1035,9 @@ bool use_pipe_mid_m(const GemmArgs& g, bool gated = false) {
          pipe_layout_ok(g);
 }
 
-// DSCQ_GEMM_TILE=<BM>x<BN>[w8] pins the tile shape (tuning sweeps only).
-template <typename OutT>
-int tile_override(const GemmArgs& g, hipStream_t stream, int* handled) {
-  static const char* env = getenv("DSCQ_GEMM_TILE");
-  *handled = 1;
-  if (env && g.KP <= 65536 && (strncmp(env, "pipe", 4) != 0 || pipe_layout_ok(g))) {
-    if (!strcmp(env, "128x256")) return launch_cfg<OutT, 128, 256, 2, 2, false>(g, stream);
-    if (!strcmp(env, "128x128")) return launch_cfg<OutT, 128, 128, 2, 2, false>(g, stream);
-    if (!strcmp(env, "256x128")) return launch_cfg<OutT, 256, 128, 2, 2, false>(g, stream);
-    if (!strcmp(env, "256x256")) return launch_cfg<OutT, 256, 256, 2, 2, false>(g, stream);
-    if (!strcmp(env, "128x256w8")) return launch_cfg<OutT, 128, 256, 2, 4, false>(g, stream);
-    if (!strcmp(env, "256x128w8")) return launch_cfg<OutT, 256, 128, 4, 2, false>(g, stream);
-    if (!strcmp(env, "64x128")) return launch_cfg<OutT, 64, 128, 2, 2, false>(g, stream);
-    if (!strcmp(env, "pipe")) return launch_pipe<OutT>(g, stream);
-    if (!strcmp(env, "gemv")) return launch_gemv<OutT>(g, stream);
-    if (!strcmp(env, "pipe128x256")) return launch_pipe_cfg<OutT, 128, 256, 2, 2, 1>(g, stream);
-    if (!strcmp(env, "pipe128")) return launch_pipe_cfg<OutT, 128, 128, 2, 2, 2>(g, stream);
-    if (!strcmp(env, "pipe64x128")) return launch_pipe_cfg<OutT, 64, 128, 2, 2, 2>(g, stream);
-    if (!strcmp(env, "pipe64x128w8")) return launch_pipe_cfg<OutT, 64, 128, 2, 4, 2>(g, stream);
-    if (!strcmp(env, "pipe128x128w8")) return launch_pipe_cfg<OutT, 128, 128, 4, 2, 2>(g, stream);
-    if (!strcmp(env, "pipe256x128w8")) return launch_pipe_cfg<OutT, 256, 128, 4, 2, 1>(g, stream);
-    if (!strcmp(env, "pipe256x128")) return launch_pipe_cfg<OutT, 256, 128, 2, 2, 1>(g, stream);
-  }
-  *handled = 0;
-  return 0;
-}
-
 template <typename OutT>
 int gemm_typed(const GemmArgs& g, bool decode, int32_t* ws, int64_t ws_bytes,
                hipStream_t stream) {
-  int handled = 0;
-  const int rc = tile_override<OutT>(g, stream, &handled);
-  if (handled) return rc;
   if (decode || g.M <= 16) return launch_gemv<OutT>(g, stream);
   // 16 < M < 64: the skinny-M kernel streams the weights once per 16 rows but
   // keeps every CU busy; the pipelined kernel's 64-row tiles pay off once N
@@ -1095,7 +1064,7 @@ int gemm_typed(const GemmArgs& g, bool decode, int32_t* ws, int64_t ws_bytes,
   return launch_cfg<OutT, 128, 128, 2, 2, false>(g, stream);
 }
 
-// Whether gemm_typed takes the pipelined kernel (tuning overrides aside).
+// Whether gemm_typed takes the pipelined kernel.
 bool takes_pipe(const GemmArgs& g, bool decode) {
   if (decode || g.M <= 16) return false;
   if (g.M < 64) return use_pipe_mid_m(g);

@@ -521,8 +521,8 @@ namespace {
 template <typename T, bool ROT, int MODE>
 int launch_rows_typed(const RowArgs& a, int wpr, int iters, hipStream_t stream) {
   if (wpr == 0) {
-    hipLaunchKernelGGL((row_quant_stream_kernel<T, ROT, MODE>), dim3((unsigned)a.MP),
-                       dim3(kThreads), 0, stream, a);
+    launch((row_quant_stream_kernel<T, ROT, MODE>), dim3((unsigned)a.MP),
+                       dim3(kThreads), stream, a);
     return launch_status("row_quant_stream_kernel");
   }
   const int rows_per_wg = (kThreads / 64) / wpr;
@@ -532,11 +532,11 @@ int launch_rows_typed(const RowArgs& a, int wpr, int iters, hipStream_t stream) 
 #define DSCQ_ROWS(W, I)                                                                   \
   if (wpr == W && iters == I) {                                                           \
     if (full && MODE == kAct)                                                             \
-      hipLaunchKernelGGL((row_quant_kernel<T, ROT, MODE, W, I, true>), grid, dim3(kThreads), \
-                         0, stream, a);                                                   \
+      launch((row_quant_kernel<T, ROT, MODE, W, I, true>), grid, dim3(kThreads), \
+                          stream, a);                                                   \
     else                                                                                  \
-      hipLaunchKernelGGL((row_quant_kernel<T, ROT, MODE, W, I, false>), grid,              \
-                         dim3(kThreads), 0, stream, a);                                   \
+      launch((row_quant_kernel<T, ROT, MODE, W, I, false>), grid,              \
+                         dim3(kThreads), stream, a);                                   \
     return launch_status("row_quant_kernel");                                            \
   }
   DSCQ_ROWS(1, 1) DSCQ_ROWS(1, 2) DSCQ_ROWS(1, 4)
@@ -593,17 +593,6 @@ int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float 
           ((K * esize) % 16 == 0);
   int wpr, iters;
   pick_shape(MP, a.nblk, &wpr, &iters);
-  // DSCQ_QUANT_SHAPE=<wpr>x<iters> pins the register-kernel shape (tuning
-  // sweeps only); it is ignored when it cannot hold the row.
-  static const char* env = getenv("DSCQ_QUANT_SHAPE");
-  if (env) {
-    int w = 0, i = 0;
-    if (sscanf(env, "%dx%d", &w, &i) == 2 && (w == 1 || w == 2 || w == 4) &&
-        (i == 1 || i == 2 || i == 4) && 16 * w * i >= a.nblk) {
-      wpr = w;
-      iters = i;
-    }
-  }
   if (!a.vec) wpr = iters = 0;  // element-wise loads: streaming kernel only
   const bool rot = rotate_block != 0;
 #define DSCQ_T(T)                                                                    \
@@ -654,11 +643,11 @@ int silu_mul_quant(const void* gate, const void* up, int64_t ld, int64_t M, int6
 #define DSCQ_GROWS(ROT, W, I)                                                                   \
   if (wpr == W && iters == I) {                                                                 \
     if (full)                                                                                   \
-      hipLaunchKernelGGL((row_quant_kernel<__half, ROT, kAct, W, I, true, true>), grid,         \
-                         dim3(kThreads), 0, stream, a);                                         \
+      launch((row_quant_kernel<__half, ROT, kAct, W, I, true, true>), grid,         \
+                         dim3(kThreads), stream, a);                                         \
     else                                                                                        \
-      hipLaunchKernelGGL((row_quant_kernel<__half, ROT, kAct, W, I, false, true>), grid,        \
-                         dim3(kThreads), 0, stream, a);                                         \
+      launch((row_quant_kernel<__half, ROT, kAct, W, I, false, true>), grid,        \
+                         dim3(kThreads), stream, a);                                         \
     return launch_status("row_quant_kernel");                                                  \
   }
 #define DSCQ_GSHAPES(ROT)                                                                       \
@@ -678,8 +667,8 @@ int silu_mul_quant(const void* gate, const void* up, int64_t ld, int64_t M, int6
 int pack_codes(const uint8_t* codes, uint8_t* packed, int64_t MP, int64_t KP,
                hipStream_t stream) {
   const int64_t n16 = MP * KP / 16;
-  hipLaunchKernelGGL(pack_codes_kernel, dim3((unsigned)((n16 + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, stream, codes, packed, n16);
+  launch(pack_codes_kernel, dim3((unsigned)((n16 + kThreads - 1) / kThreads)),
+                     dim3(kThreads), stream, codes, packed, n16);
   return launch_status("pack_codes_kernel");
 }
 
@@ -687,8 +676,8 @@ int pack_int4(const int8_t* codes, int64_t R, int64_t C, uint8_t* packed,
               hipStream_t stream) {
   const int64_t n = R * ((C + 1) / 2);
   if (n == 0) return DSCQ_OK;
-  hipLaunchKernelGGL(pack_int4_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, stream, codes, R, C, packed);
+  launch(pack_int4_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
+                     dim3(kThreads), stream, codes, R, C, packed);
   return launch_status("pack_int4_kernel");
 }
 
@@ -696,8 +685,8 @@ int unpack_int4(const uint8_t* packed, int64_t R, int64_t CB, int64_t width,
                 int8_t* codes, hipStream_t stream) {
   const int64_t n = R * width;
   if (n == 0) return DSCQ_OK;
-  hipLaunchKernelGGL(unpack_int4_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, stream, packed, R, CB, width, codes);
+  launch(unpack_int4_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
+                     dim3(kThreads), stream, packed, R, CB, width, codes);
   return launch_status("unpack_int4_kernel");
 }
 

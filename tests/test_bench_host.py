@@ -104,3 +104,14 @@ def test_more_than_one_gpu_is_refused():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr or "single" in r.stderr
+
+
+def test_cpu_baseline_threads_follow_the_process_share(monkeypatch):
+    import bench
+    monkeypatch.setenv("OMP_NUM_THREADS", "3")
+    n, share = bench.cpu_threads()
+    assert n == min(3, len(os.sched_getaffinity(0)))
+    assert "OMP_NUM_THREADS=3" in share or n == (os.cpu_count() or 1)
+    monkeypatch.delenv("OMP_NUM_THREADS")
+    n, _ = bench.cpu_threads()
+    assert n == len(os.sched_getaffinity(0))

@@ -1,5 +1,6 @@
-"""Full-size parity at the Llama-70B linear shapes (M=4096; K=N=8192 and
-K=28672 -> N=8192), where a whole-output oracle product would be slow.
+"""Full-size parity at the Llama-70B linear shapes (M=4096; q/o K=N=8192,
+gate/up K=8192 -> N=28672, down K=28672 -> N=8192), where a whole-output
+oracle product would be slow.
 
 The activation quantization (rotate + quantize + pack, 4096 x 28672) and the
 weight packing are checked bit for bit against the oracle in full; the GEMM's
@@ -27,7 +28,7 @@ def _activations(M, K, seed):
     return x.half()
 
 
-@pytest.mark.parametrize("M,N,K", [(4096, 8192, 8192), (4096, 8192, 28672)])
+@pytest.mark.parametrize("M,N,K", [(4096, 8192, 8192), (4096, 28672, 8192), (4096, 8192, 28672)])
 def test_70b_shapes_full_quantize_and_sampled_gemm(gpu, M, N, K):
     print(f"70B-shape case M{M} N{N} K{K}", flush=True)
     rot = 128

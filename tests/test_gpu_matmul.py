@@ -82,6 +82,10 @@ MM_CASES = [
     # K split over workgroups (few 64 x 128 tiles, long K): 4 and 5 parts
     (130, 2056, 8384, True, True, False),
     (64, 4104, 11072, False, False, False),
+    # K split with an fp16 bias: mid-M (pipelined 64 x 128 tiles, 2 parts) and
+    # M = 128 down projection (4 parts)
+    (32, 11008, 11008, True, False, False),
+    (128, 4096, 11008, True, False, False),
 ]
 
 

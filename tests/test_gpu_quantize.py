@@ -43,6 +43,10 @@ QUANT_CASES = [
     (100, 4096, np.float16, 0, 0.75, False),
     (37, 1024, np.float32, 128, 1.0, True),
     (37, 1000, np.float32, 0, 0.9, False),
+    # two-pass with the online rotation (codes kernel + pack kernel)
+    (2048, 4096, np.float16, 128, 1.0, False),
+    (19, 11008, np.float32, 128, 0.75, False),
+    (3, 40064, np.float16, 128, 1.0, False),
     # ragged / tiny K (scalar load path), padded rows
     (5, 100, np.float16, 0, 1.0, True),
     (9, 1, np.float16, 0, 1.0, True),

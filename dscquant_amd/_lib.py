@@ -34,6 +34,8 @@ SIGNATURES = {
     "dscq_matmul": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P, _P],
     "dscq_matmul_ws": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P,
                        _P, _I64, _P],
+    "dscq_matmul_noalloc": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _P,
+                            _P],
     "dscq_matmul_workspace_bytes": [_I64, _I64, _I64, _I],
     "dscq_linear_decode": [_P, _I, _I64, _I64, _F, _I, _P, _P, _P, _P, _I64, _I, _P, _P],
     "dscq_linear_decode_supported": [_I64, _I64],

@@ -188,6 +188,23 @@ int dscq_matmul_ws(const uint8_t* a, const uint8_t* b, const float* sx,
                    int force_decode, int out_fp32, void* out, int32_t* raw,
                    void* workspace, int64_t workspace_bytes, void* stream);
 
+/* dscq_matmul that allocates nothing: no counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture that forbids allocation, tight serving loops, harnesses that forbid
+ * hipMalloc).  Arguments, errors and results are dscq_matmul's (bit-identical
+ * to dscq_matmul_ws with a workspace).  The K split's int32 partial sums go
+ * to a fixed device array of the library, DSCQ_NOALLOC_SCRATCH_BYTES per GPU,
+ * held until the process ends; a shape whose split would need more returns
+ * DSCQ_EINVAL (on a 256-CU MI355X no shape does).  Calls on one GPU share
+ * that array, so calls that may overlap on one GPU race: serialize them on
+ * one stream.  Nothing in it needs clearing between calls. */
+#define DSCQ_NOALLOC_SCRATCH_BYTES (8LL << 20)
+int dscq_matmul_noalloc(const uint8_t* a, const uint8_t* b, const float* sx,
+                        const int32_t* zx, const float* sw, const int32_t* sums,
+                        const void* bias, int64_t M, int64_t N, int64_t KP, int fused,
+                        int force_decode, int out_fp32, void* out, int32_t* raw,
+                        void* stream);
+
 /* Bytes of workspace dscq_matmul_ws uses for this shape (0: it does not split;
  * the workspace may then be NULL), or a negative value for invalid dimensions
  * (as dscq_matmul reports them).  Host-only: launches nothing. */

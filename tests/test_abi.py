@@ -103,6 +103,17 @@ def test_c_matmul_ws_argument_checks_and_workspace_query():
     assert w4a4.workspace_bytes(128, 4096, 11008) == 4 * 128 * 4096 * 4
 
 
+def test_c_matmul_noalloc_argument_checks():
+    d = 16
+    for M, N, KP in ((0, 8, 64), (65536, 8, 64), (4, 0, 64), (4, 8, 96)):
+        assert _einval("dscq_matmul_noalloc", d, d, d, d, d, d, None, M, N, KP, 1, 0, 0, d,
+                       None, None) == "Invalid dimensions"
+    assert "raw buffer" in _einval("dscq_matmul_noalloc", d, d, d, d, d, d, None, 4, 8, 64, 0,
+                                   0, 0, d, None, None)
+    assert "null buffer" in _einval("dscq_matmul_noalloc", None, d, d, d, d, d, None, 4, 8, 64,
+                                    1, 0, 0, d, None, None)
+
+
 def test_c_other_argument_checks():
     d = 16
     assert "bits" in _einval("dscq_activation_codes", d, 0, 4, 64, 1.0, 9, 0, d, d, d, None)

@@ -63,9 +63,11 @@ __device__ __forceinline__ float readlane_f32(float v, int lane) {
 // Min / max over the 64 lanes of a wave; every lane gets the result.  Each
 // 16-lane row is reduced with v_min / v_max taking one operand through DPP
 // (one instruction per step; written out because the compiler pairs a DPP
-// move with a canonicalizing max before every fminf / fmaxf).  The leading
-// s_nop covers the two wait states gfx9 needs between a VALU write and a DPP
-// read of the same register.  Inputs are finite.
+// move with a canonicalizing max before every fminf / fmaxf), then
+// row_bcast:15 folds row 0 into row 1 and row 2 into row 3, row_bcast:31 rows
+// 0-1 into rows 2-3, leaving the wave's result in lane 63.  The s_nops cover
+// the two wait states gfx9 needs between a VALU write and a DPP read of the
+// same register.  Inputs are finite.
 #define DSCQ_DPP_REDUCE(OP, V)                                                         \
   asm("s_nop 1\n\t"                                                                   \
       "v_" OP "_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"  \
@@ -74,19 +76,21 @@ __device__ __forceinline__ float readlane_f32(float v, int lane) {
       "s_nop 1\n\t"                                                                   \
       "v_" OP "_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"            \
       "s_nop 1\n\t"                                                                   \
-      "v_" OP "_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf"                  \
+      "v_" OP "_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"            \
+      "s_nop 1\n\t"                                                                   \
+      "v_" OP "_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"         \
+      "s_nop 1\n\t"                                                                   \
+      "v_" OP "_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf"              \
       : "+v"(V))
 
 __device__ __forceinline__ float wave_min(float v) {
   DSCQ_DPP_REDUCE("min", v);
-  return fminf(fminf(readlane_f32(v, 0), readlane_f32(v, 16)),
-               fminf(readlane_f32(v, 32), readlane_f32(v, 48)));
+  return readlane_f32(v, 63);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
   DSCQ_DPP_REDUCE("max", v);
-  return fmaxf(fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)),
-               fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
+  return readlane_f32(v, 63);
 }
 #undef DSCQ_DPP_REDUCE
 

@@ -111,17 +111,32 @@ __device__ __forceinline__ void write_row_meta(const RowArgs& a, int64_t row, bo
   }
 }
 
-// FULL: every chunk of every quad lies inside K (K == nblk * 128 and
-// nblk == 16 * WPR * ITERS), so no per-chunk masking is needed.
+// FIT describes how the row fills the blocks the quads walk:
+//   kFull   every quad has a whole block in every iteration (K == nblk * 128
+//           == 16 * WPR * ITERS * 128): no masking and no per-iteration tests;
+//   kWhole  K == nblk * 128, so every 128-block is complete, but the quads
+//           walk past the row's last block.  Those blocks are handled per
+//           iteration at wave granularity: an iteration none of whose quads
+//           has a block skips its arithmetic and stores (a uniform branch);
+//           one whose quads are partly past the row zeroes those quads' chunks;
+//   kPart   the last block is partial as well: every iteration is masked.
+// CLAMP (activations): 0 when clip == 1 and qmax == 15, whose codes need no
+// clamp (act_chunk_fast_noclamp), else 1.
 // Gated input (the SiLU-gated MLP between its up and down projections): the
 // row is h = silu_mul_f16x2(g, u) (rowquant.h) of two fp16 rows g (x) and u (up).
 
-template <typename T, bool ROT, int MODE, int WPR, int ITERS, bool FULL, bool GATED = false>
+enum Fit { kPart = 0, kWhole = 1, kFull = 2 };
+
+template <typename T, bool ROT, int MODE, int WPR, int ITERS, int FIT, int CLAMP,
+          bool GATED = false>
 __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
+  constexpr bool WHOLE = FIT != kPart, FULL = FIT == kFull;
   constexpr int ROWS = (kThreads / 64) / WPR;
   constexpr int NQ = 16 * WPR;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform values in scalar registers: the row's base address is then
+  // the scalar base of every load and store of the wave.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row_in_wg = wave / WPR;
   const int wave_in_row = wave % WPR;
   const int64_t row = (int64_t)blockIdx.x * ROWS + row_in_wg;
@@ -131,17 +146,30 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
   const int r = lane & 3;
   const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.ldx;
 
+  // Per iteration, uniform over the wave: does any quad have a block (wlive),
+  // and are some quads past the row (wmix)?  Padded rows compute nothing.
+  bool wlive[ITERS], wmix[ITERS];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int first = wave_in_row * 16 + it * NQ;
+    wlive[it] = real && (FULL || first < a.nblk);
+    wmix[it] = !FULL && first + 15 >= a.nblk;
+  }
+  auto quad_ok = [&](int it, int j) {
+    const int b = quad + it * NQ;
+    const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
+    return FULL || (b < a.nblk && (WHOLE || e0 < a.K));
+  };
+
   // Rows of this kernel are 16-byte aligned with K % 8 == 0 (see row_quant).
+  // Loads are unconditional (out-of-range chunks read element 0 of the row),
+  // so every load of a lane is in flight at once.
   Raw<T> raw[ITERS][4];
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     const int b = quad + it * NQ;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
-      const bool ok = FULL || (b < a.nblk && e0 < a.K);
-      raw[it][j] = load_raw<T>(xrow, e0, ok);
-    }
+    for (int j = 0; j < 4; ++j) raw[it][j] = load_raw32<T>(xrow, b * 128 + j * 32 + r * 8, quad_ok(it, j));
   }
   if (GATED) {
     static_assert(!GATED || sizeof(T) == 2, "gated rows are fp16");
@@ -151,10 +179,8 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
     for (int it = 0; it < ITERS; ++it) {
       const int b = quad + it * NQ;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
-        rup[it][j] = load_raw<T>(urow, e0, FULL || (b < a.nblk && e0 < a.K));
-      }
+      for (int j = 0; j < 4; ++j)
+        rup[it][j] = load_raw32<T>(urow, b * 128 + j * 32 + r * 8, quad_ok(it, j));
     }
 #pragma unroll
     for (int it = 0; it < ITERS; ++it)
@@ -166,30 +192,34 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
         for (int k = 0; k < 4; ++k) w[k] = silu_mul_f16x2(w[k], wu[k]);
       }
   }
-  // Zero what was loaded from a placeholder address: padded rows (uniform per
-  // wave) and, unless FULL, chunks past the end of the row.
-  const bool zero_row = !real;
+
+  float v[ITERS][4][8];
+  float mn = 0.0f, mx = 0.0f;
+  // Lane sign after the signed transform (values held are lsign * y).
+  const float lsign = (ROT && (r == 1 || r == 2)) ? -1.0f : 1.0f;
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
-    const int b = quad + it * NQ;
+    if (!wlive[it]) continue;
+    // Zero the chunks loaded from the placeholder address.
+    if (!WHOLE || wmix[it]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t e0 = (int64_t)b * 128 + j * 32 + r * 8;
-      const bool ok = !zero_row && (FULL || (b < a.nblk && e0 < a.K));
-      if (!FULL || zero_row) {
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = quad_ok(it, j);
         uint32_t* w = reinterpret_cast<uint32_t*>(&raw[it][j]);
 #pragma unroll
         for (int k = 0; k < (int)(sizeof(Raw<T>) / 4); ++k) w[k] = ok ? w[k] : 0u;
       }
-      if (GATED && a.hout && real && (FULL || (b < a.nblk && e0 < a.K)))
-        *reinterpret_cast<uint4*>(a.hout + row * a.K + e0) = *reinterpret_cast<const uint4*>(&raw[it][j]);
     }
-  }
-
-  float v[ITERS][4][8];
-  if (ROT && sizeof(T) == 2) {
+    if (GATED && a.hout) {
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it)
+      for (int j = 0; j < 4; ++j) {
+        const int64_t e0 = (int64_t)(quad + it * NQ) * 128 + j * 32 + r * 8;
+        if (quad_ok(it, j))
+          *reinterpret_cast<uint4*>(a.hout + row * a.K + e0) =
+              *reinterpret_cast<const uint4*>(&raw[it][j]);
+      }
+    }
+    if (ROT && sizeof(T) == 2) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t* w = reinterpret_cast<const uint32_t*>(&raw[it][j]);
@@ -197,20 +227,14 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
         for (int k = 0; k < 4; ++k) bfly_f16x2(w[k], v[it][j][2 * k], v[it][j][2 * k + 1]);
         fwht_chunk_tail(v[it][j]);
       }
-  } else {
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it)
+    } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         to_f32(raw[it][j], v[it][j]);
         if (ROT) fwht_chunk(v[it][j]);
       }
-  }
-  // Lane sign after the signed transform (values held are lsign * y).
-  const float lsign = (ROT && (r == 1 || r == 2)) ? -1.0f : 1.0f;
-  if (ROT) {
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
+    }
+    if (ROT) {
       fwht_block_tail_signed(v[it], r);
       if (MODE == kWgt) {
 #pragma unroll
@@ -219,11 +243,6 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
           for (int i = 0; i < 8; ++i) v[it][j][i] *= 0.0078125f;  // 1/128, exact
       }
     }
-  }
-
-  float mn = 0.0f, mx = 0.0f;
-#pragma unroll
-  for (int it = 0; it < ITERS; ++it)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -235,6 +254,7 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
           mx = fmaxf(mx, fabsf(v[it][j][i]));
         }
       }
+  }
   if (MODE == kAct && ROT) {
     // Undo the lane sign: min / max of -y are -max / -min of y.
     const float mn_l = mn, mx_l = mx;
@@ -258,90 +278,94 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
       mx = fmaxf(mx, red[1][row_in_wg * WPR + w]);
     }
   }
-  const RowScale rs = row_scale<MODE>(mn, mx, a.clip, a.qmax);
+  RowScale rs = row_scale<MODE>(mn, mx, a.clip, a.qmax);
+  // The zero point and the guard threshold are uniform over the wave: keep
+  // them in scalar registers (operands of every chunk's fma and compare).
+  rs.zf = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, rs.zf)));
+  rs.thr = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, rs.thr)));
   // Lanes holding -y: the fast path folds the sign into the reciprocal
   // ((-y) * (-1/s) == y * (1/s) exactly); the exact path and the weight path
   // negate the values back first.
   RowScale rs_l = rs;
   rs_l.y = lsign * rs.y;
-  auto unsign = [&]() {
-    if (ROT && lsign < 0.0f) {
-#pragma unroll
-      for (int it = 0; it < ITERS; ++it)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) v[it][j][i] = -v[it][j][i];
-    }
-  };
 
   uint32_t ev[ITERS][4], od[ITERS][4];
   int sum = 0;
-  if (MODE == kAct) {
-    const bool noclamp = a.clip == 1.0f && a.qmax == 15.0f;
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it)
+  for (int it = 0; it < ITERS; ++it) {
+    if (!wlive[it]) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 4; ++j) {
+      if (MODE == kAct) {
         float dmax = 0.0f;
-        if (noclamp)
-          act_chunk_fast_noclamp(v[it][j], rs_l, ev[it][j], od[it][j], dmax);
-        else
+        if (CLAMP)
           act_chunk_fast(v[it][j], rs_l, ev[it][j], od[it][j], dmax);
+        else
+          act_chunk_fast_noclamp(v[it][j], rs_l, ev[it][j], od[it][j], dmax);
         if (dmax >= rs.thr) act_chunk_exact(v[it][j], rs, lsign, ev[it][j], od[it][j]);
+      } else {
+        if (ROT && lsign < 0.0f) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[it][j][i] = -v[it][j][i];
+        }
+        wgt_chunk(v[it][j], rs, ev[it][j], od[it][j], sum);
       }
-  } else {
-    unsign();
+    }
+  }
+  if (MODE == kWgt && a.sums) {
+    sum = wave_sum_i32(sum);
+    if (WPR > 1) {
+      // Reached by every wave of the workgroup (no early exits above).
+      __shared__ int sred[kThreads / 64];
+      if (lane == 0) sred[wave] = sum;
+      __syncthreads();
+      sum = 0;
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) wgt_chunk(v[it][j], rs, ev[it][j], od[it][j], sum);
-    if (a.sums) {
-      sum = wave_sum_i32(sum);
-      if (WPR > 1) {
-        // Reached by every wave of the workgroup (no early exits above).
-        __shared__ int sred[kThreads / 64];
-        if (lane == 0) sred[wave] = sum;
-        __syncthreads();
-        sum = 0;
-#pragma unroll
-        for (int w = 0; w < WPR; ++w) sum += sred[row_in_wg * WPR + w];
-      }
+      for (int w = 0; w < WPR; ++w) sum += sred[row_in_wg * WPR + w];
     }
   }
   if (!live) return;
 
-  // Row base computed once; e0 < KP <= 2^20 fits 32 bits; with FULL every
-  // chunk lies inside KP.  The unpacked codes (two-step mode) in their own
-  // uniform branch, so the packed stores are straight-line.
+  // Padded rows (real == false) computed nothing: every code is the zero
+  // point 0 (activations) or 0 (weights), stored as u = 0 / qmax + 1.
+  if (!real) {
+    const uint32_t u = MODE == kAct ? 0u : 0x01010101u * (uint32_t)(a.qmax + 1.0f);
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ev[it][j] = u;
+        od[it][j] = u;
+      }
+  }
+  // Row base computed once (uniform); e0 < KP <= 2^20 fits 32 bits.  Stores
+  // are checked per chunk only in iterations whose quads run past the row.
+  // The unpacked codes (two-step mode) in their own uniform branch, so the
+  // packed stores are straight-line.
+  auto checked = [&](int it, int j) {
+    const int b = quad + it * NQ;
+    const int e0 = b * 128 + j * 32 + r * 8;
+    return b < a.nblk && (WHOLE || e0 < a.KP);
+  };
+  auto store_iters = [&](auto&& store_one) {
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      if (!(wlive[it] || !real)) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e0 = (quad + it * NQ) * 128 + j * 32 + r * 8;
+        if (FULL || (WHOLE && !wmix[it]) || checked(it, j)) store_one(it, j, e0);
+      }
+    }
+  };
   if (a.packed) {
     uint8_t* const prow = a.packed + row * (a.KP / 2);
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-      const int b = quad + it * NQ;
-      if (FULL || b < a.nblk) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int e0 = b * 128 + j * 32 + r * 8;
-          if (FULL || e0 < a.KP)
-            *reinterpret_cast<uint32_t*>(prow + e0 / 2) = packed_nibbles(ev[it][j], od[it][j]);
-        }
-      }
-    }
+    store_iters([&](int it, int j, int e0) {
+      *reinterpret_cast<uint32_t*>(prow + (uint32_t)e0 / 2u) = packed_nibbles(ev[it][j], od[it][j]);
+    });
   }
-  if (a.codes) {
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-      const int b = quad + it * NQ;
-      if (FULL || b < a.nblk) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int e0 = b * 128 + j * 32 + r * 8;
-          if (FULL || e0 < a.KP) store_codes<MODE>(a, row, e0, ev[it][j], od[it][j]);
-        }
-      }
-    }
-  }
+  if (a.codes)
+    store_iters([&](int it, int j, int e0) { store_codes<MODE>(a, row, e0, ev[it][j], od[it][j]); });
   if (wave_in_row == 0 && lane == 0) write_row_meta<MODE>(a, row, real, rs, sum);
 }
 
@@ -527,16 +551,22 @@ int launch_rows_typed(const RowArgs& a, int wpr, int iters, hipStream_t stream) 
   }
   const int rows_per_wg = (kThreads / 64) / wpr;
   const dim3 grid((unsigned)((a.MP + rows_per_wg - 1) / rows_per_wg));
-  // Full rows: K fills exactly the 16 * wpr * iters blocks every quad walks.
-  const bool full = a.K == (int64_t)a.nblk * 128 && a.nblk == 16 * wpr * iters;
+  // How the row fills the quads' blocks; clip 1 at 4 bits needs no clamp.
+  const bool whole = a.K == (int64_t)a.nblk * 128;
+  const bool full = whole && a.nblk == 16 * wpr * iters;
+  const bool noclamp = MODE == kAct && a.clip == 1.0f && a.qmax == 15.0f;
 #define DSCQ_ROWS(W, I)                                                                   \
   if (wpr == W && iters == I) {                                                           \
-    if (full && MODE == kAct)                                                             \
-      launch((row_quant_kernel<T, ROT, MODE, W, I, true>), grid, dim3(kThreads), \
-                          stream, a);                                                   \
+    if (MODE == kAct && full && noclamp)                                                  \
+      launch((row_quant_kernel<T, ROT, MODE, W, I, kFull, 0>), grid, dim3(kThreads), stream, a); \
+    else if (MODE == kAct && full)                                                        \
+      launch((row_quant_kernel<T, ROT, MODE, W, I, kFull, 1>), grid, dim3(kThreads), stream, a); \
+    else if (MODE == kAct && whole && noclamp)                                            \
+      launch((row_quant_kernel<T, ROT, MODE, W, I, kWhole, 0>), grid, dim3(kThreads), stream, a); \
+    else if (whole)                                                                       \
+      launch((row_quant_kernel<T, ROT, MODE, W, I, kWhole, 1>), grid, dim3(kThreads), stream, a); \
     else                                                                                  \
-      launch((row_quant_kernel<T, ROT, MODE, W, I, false>), grid,              \
-                         dim3(kThreads), stream, a);                                   \
+      launch((row_quant_kernel<T, ROT, MODE, W, I, kPart, 1>), grid, dim3(kThreads), stream, a); \
     return launch_status("row_quant_kernel");                                            \
   }
   DSCQ_ROWS(1, 1) DSCQ_ROWS(1, 2) DSCQ_ROWS(1, 4)
@@ -639,15 +669,21 @@ int silu_mul_quant(const void* gate, const void* up, int64_t ld, int64_t M, int6
     return fail("silu_mul_quantize: need N %% 8 == 0, N <= 32768 and 16-byte aligned rows");
   const int rows_per_wg = (kThreads / 64) / wpr;
   const dim3 grid((unsigned)((a.MP + rows_per_wg - 1) / rows_per_wg));
-  const bool full = a.K == (int64_t)a.nblk * 128 && a.nblk == 16 * wpr * iters;
+  const bool whole = a.K == (int64_t)a.nblk * 128;
+  const bool full = whole && a.nblk == 16 * wpr * iters;
+  const int fit = full ? kFull : whole ? kWhole : kPart;
+  const bool noclamp = a.clip == 1.0f;
 #define DSCQ_GROWS(ROT, W, I)                                                                   \
   if (wpr == W && iters == I) {                                                                 \
-    if (full)                                                                                   \
-      launch((row_quant_kernel<__half, ROT, kAct, W, I, true, true>), grid,         \
-                         dim3(kThreads), stream, a);                                         \
+    if (fit == kFull && noclamp)                                                                \
+      launch((row_quant_kernel<__half, ROT, kAct, W, I, kFull, 0, true>), grid, dim3(kThreads), \
+             stream, a);                                                                        \
+    else if (fit == kWhole && noclamp)                                                          \
+      launch((row_quant_kernel<__half, ROT, kAct, W, I, kWhole, 0, true>), grid, dim3(kThreads),\
+             stream, a);                                                                        \
     else                                                                                        \
-      launch((row_quant_kernel<__half, ROT, kAct, W, I, false, true>), grid,        \
-                         dim3(kThreads), stream, a);                                         \
+      launch((row_quant_kernel<__half, ROT, kAct, W, I, kPart, 1, true>), grid, dim3(kThreads), \
+             stream, a);                                                                        \
     return launch_status("row_quant_kernel");                                                  \
   }
 #define DSCQ_GSHAPES(ROT)                                                                       \

@@ -54,6 +54,24 @@ __device__ __forceinline__ Raw<__half> load_raw<__half>(const __half* row, int64
   return r;
 }
 
+// The same with a 32-bit element offset (rows of at most 2^28 elements): the
+// wave-uniform row base and a per-lane byte offset map onto one
+// global_load_dwordx4 with scalar base and vector offset, with no 64-bit
+// address arithmetic per load.
+template <typename T>
+__device__ __forceinline__ Raw<T> load_raw32(const T* row, int e0, bool ok) {
+  const uint32_t off = (uint32_t)(ok ? e0 : 0) * (uint32_t)sizeof(T);
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(row);
+  Raw<T> r;
+  if constexpr (sizeof(T) == 2) {
+    r.w = *reinterpret_cast<const uint4*>(base + off);
+  } else {
+    r.w0 = *reinterpret_cast<const uint4*>(base + off);
+    r.w1 = *reinterpret_cast<const uint4*>(base + off + 16);
+  }
+  return r;
+}
+
 template <>
 __device__ __forceinline__ Raw<float> load_raw<float>(const float* row, int64_t e0,
                                                       bool ok) {

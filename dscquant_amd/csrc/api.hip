@@ -49,6 +49,22 @@ KernelEvents take_kernel_events() {
   return ev;
 }
 
+void arm_kernel_events(KernelEvents ev) { g_kernel_events = ev; }
+
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 int fail(const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -120,9 +136,13 @@ int dscq_quantize(const void* x, int x_dtype, int64_t M, int64_t K, float clip, 
   if (fused)
     return row_quant(x, x_dtype, M, K, MP, clip, 0, 15.0f, rotate_block, packed, nullptr,
                      scales, zeros, nullptr, s);
+  // Two kernels: timing events, if armed, span both.
+  const KernelEvents ev = take_kernel_events();
+  arm_kernel_events({ev.start, nullptr});
   if (int rc = row_quant(x, x_dtype, M, K, MP, clip, 0, 15.0f, rotate_block, nullptr,
                          codes, scales, zeros, nullptr, s))
     return rc;
+  arm_kernel_events({nullptr, ev.stop});
   return pack_codes(codes, packed, MP, KP, s);
 }
 

@@ -18,6 +18,8 @@ int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 int launch_status(const char* what);
 
 inline int64_t ceil_to(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+// Compute units of the current device (cached per device; 256 on MI355X).
+int cu_count();
 
 // Events armed by dscq_time_next_kernel for this thread's next kernel launch
 // (both null when none is armed); taking them disarms them.
@@ -25,6 +27,9 @@ struct KernelEvents {
   hipEvent_t start, stop;
 };
 KernelEvents take_kernel_events();
+// Arms events for the next launch (used to hand the stop event of a call to
+// its last kernel).
+void arm_kernel_events(KernelEvents ev);
 
 // Every kernel of the library is launched through here.  With events armed the
 // launch goes through hipExtLaunchKernel, which stamps the kernel's own start

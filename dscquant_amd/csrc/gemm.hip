@@ -697,21 +697,6 @@ int launch_pipe_cfg(GemmArgs g, hipStream_t stream) {
   return launch_status("w4a4_gemm_pipe_kernel");
 }
 
-// Compute units of the current device (cached per device; 256 on MI355X).
-int cu_count() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 // Tile choice.  256 x 128 tiles (one workgroup per CU, two waves per SIMD)
 // move the least data per MFMA and win whenever their rounds of one tile per
 // CU are well filled (a whole number of rounds, a last round more than 60%
@@ -826,6 +811,10 @@ int launch_pipe_split(GemmArgs g, int parts, int32_t* ws, hipStream_t stream) {
   if ((quads + 255) / 256 > 0x7FFFFFFF) return fail("matmul: grid too large");
   const bool ktail = (g.KP / 2) % 128 != 0;
   const dim3 grid((unsigned)(g.tiles * parts)), block(512);
+  // Timing events armed for this call: the split kernel stamps the start, the
+  // reduce kernel the end.
+  const KernelEvents ev = take_kernel_events();
+  arm_kernel_events({ev.start, nullptr});
   if (ktail)
     launch((w4a4_gemm_pipe_kernel<OutT, 64, 128, 2, 4, 2, true, false, false, true>),
                        grid, block, stream, g);
@@ -835,6 +824,7 @@ int launch_pipe_split(GemmArgs g, int parts, int32_t* ws, hipStream_t stream) {
   const int rc = launch_status("w4a4_gemm_pipe_kernel");
   if (rc) return rc;
   const dim3 rgrid((unsigned)((quads + 255) / 256)), rblock(256);
+  arm_kernel_events({nullptr, ev.stop});
   if (g.bias)
     launch((w4a4_split_reduce_kernel<OutT, true>), rgrid, rblock, stream, g, parts);
   else

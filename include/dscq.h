@@ -256,15 +256,16 @@ int dscq_linear_decode_supported(int64_t M, int64_t K);
 int dscq_device_supported(void);
 
 /*
- * Kernel timing without a profiler (no reference counterpart): the next kernel
- * the calling thread launches through this library stamps its own device start
- * and end times into the HIP events `start` and `stop` (hipEvent_t created
+ * Kernel timing without a profiler (no reference counterpart): the next call
+ * the calling thread makes into this library stamps the device start and end
+ * times of its kernel into the HIP events `start` and `stop` (hipEvent_t created
  * with timing enabled; either may be NULL).  The launch goes through
  * hipExtLaunchKernel, so hipEventElapsedTime(start, stop) is the kernel's
  * duration as a kernel trace reports it, without the event markers and
- * dispatch gaps of events recorded around the call.  One launch only: an entry
- * point that launches two kernels (a K-split matmul) times the first.  Not for
- * use under graph capture.
+ * dispatch gaps of events recorded around the call.  An entry point that
+ * launches two kernels (a K-split matmul: partial sums, then their reduction)
+ * stamps the start of the first and the end of the second.  Not for use under
+ * graph capture.
  */
 int dscq_time_next_kernel(void* start, void* stop);
 

@@ -38,6 +38,12 @@ QUANT_CASES = [
     (64, 8192, np.float16, 128, 1.0, True),
     (24, 28672, np.float16, 128, 1.0, True),
     (3, 28672, np.float16, 0, 1.0, True),
+    # the row-pipelined kernel (two or four rows per wave): padded rows, clip < 1,
+    # fp32, 2048 / 8192 elements
+    (2045, 4096, np.float16, 128, 1.0, True),
+    (4100, 2048, np.float16, 0, 0.75, True),
+    (2048, 4096, np.float32, 128, 1.0, True),
+    (4096, 8192, np.float16, 128, 1.0, True),
     # clip, dtype, two-pass
     (100, 4096, np.float16, 128, 0.5, True),
     (100, 4096, np.float16, 0, 0.75, False),

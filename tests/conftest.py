@@ -11,6 +11,14 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    # tests/sanitize_host.py runs the CPU tests against sanitized builds of the
+    # oracle and of libdscq's host side; these variables name those builds.
+    if os.environ.get("DSCQ_TEST_ORACLE_LIB"):
+        from oracle import native
+        native.LIB_PATH = os.environ["DSCQ_TEST_ORACLE_LIB"]
+    if os.environ.get("DSCQ_TEST_LIBDSCQ"):
+        from dscquant_amd import _lib
+        _lib.LIB_PATH = os.environ["DSCQ_TEST_LIBDSCQ"]
 
 
 @pytest.fixture(scope="session", autouse=True)

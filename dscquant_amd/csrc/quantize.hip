@@ -361,7 +361,7 @@ __global__ __launch_bounds__(kThreads) void row_quant_kernel(RowArgs a) {
   if (a.packed) {
     uint8_t* const prow = a.packed + row * (a.KP / 2);
     store_iters([&](int it, int j, int e0) {
-      *reinterpret_cast<uint32_t*>(prow + (uint32_t)e0 / 2u) = packed_nibbles(ev[it][j], od[it][j]);
+      store_stream(packed_nibbles(ev[it][j], od[it][j]), prow + (uint32_t)e0 / 2u);
     });
   }
   if (a.codes)

@@ -11,8 +11,18 @@
 //   2. quantizes all M activation rows itself -- the same per-element
 //      arithmetic as the quantize kernel (rowquant.h), so codes, scales and
 //      zero-points are bit-identical -- into LDS, while the weights arrive;
-//   3. runs the int8-MFMA dot products from LDS and registers and applies the
-//      reference's epilogue (kernel/w4a4.cu:70-78, 156-161).
+//   3. runs the dot products and applies the reference's epilogue
+//      (kernel/w4a4.cu:70-78, 156-161).  Two forms:
+//        MFMA (M >= 3): int8 MFMAs over the unpacked nibbles, the 16 columns
+//          as one 16 x 16 tile, each wave on a K range, sums meeting in LDS;
+//        DOT (M <= 2): v_dot8_i32_i4 (eight signed-nibble products per
+//          instruction, straight on the packed bytes: both operands already
+//          hold two's-complement nibbles, (q - 8) & 15 and c & 15), each wave
+//          on two of the 16 columns over all of K, so no sums cross waves.
+//          Measured against MFMA (graph-replayed, weights from HBM, identical
+//          outputs): M = 1, K = N = 4096 4.70 / 4.72 us; M = 1, N = 11008
+//          6.87 / 7.50 us; M = 1, K = 11008 7.36 / 9.20 us; M = 2 5.58 /
+//          5.76 us; M = 4 6.20 / 5.74 us (there the MFMA's 16 rows win).
 // The quantization is repeated by every workgroup; it is cheap only while
 // M * ceil(K / 128) <= 128 (one 128-element block per quad of lanes), which
 // is the limit this kernel accepts (decode: M <= 4 at K = 4096, M = 1 up to
@@ -33,7 +43,9 @@ namespace {
 
 constexpr int kWaves = 8;                 // workgroup = 8 waves = 32 blocks of 16 lanes
 constexpr int kMaxBlocks = 128;           // activation blocks (M * nblk)
-constexpr int kMaxBlocksPerWave = 12;     // 64-byte k blocks of b per wave (max)
+constexpr int kMaxBlocksPerWave = 12;     // MFMA form: 64-byte k blocks of b per wave (max)
+constexpr int kMaxPieces = 12;            // DOT form: 16-byte pieces of a weight row per lane
+constexpr int kDotMaxRows = 2;            // DOT form for M <= 2
 constexpr int kMaxABytes = 16384;         // LDS for the packed activations
 
 struct DecodeArgs {
@@ -65,9 +77,11 @@ __device__ __forceinline__ void bfly_swizzle(float (&c)[8], float sgn) {
   }
 }
 
-// PER: weight blocks held per wave (4, 8 or 12 >= the blocks a wave owns),
-// a compile-time count so the loads are unconditional -- a load behind a
-// branch makes the wait for an earlier load conservative.
+// PER: weight pieces held per lane -- MFMA form: 64-byte blocks per wave (4,
+// 8 or 12 >= the blocks a wave owns); DOT form: 16-byte pieces of the lane's
+// weight row (4, 8 or 12 >= ceil(KB / 512)) -- a compile-time count so the
+// loads are unconditional: a load behind a branch makes the wait for an
+// earlier load conservative.
 //
 // Activation layouts (both run the quantize kernel's butterflies in the same
 // order, so every value is rounded identically; rowquant.h):
@@ -79,12 +93,12 @@ __device__ __forceinline__ void bfly_swizzle(float (&c)[8], float sgn) {
 //     (pairs share r, hence the sign).  8 elements per lane per pass.
 //   QUAD (ITERS = 0, M * nblk <= 128): the quantize kernel's layout, a block
 //     per quad of lanes, 32 elements per lane, bits 5-6 in the lane.
-template <typename T, typename OutT, bool ROT, bool BIAS, int PER, int ITERS>
+template <typename T, typename OutT, bool ROT, bool BIAS, int PER, int ITERS, bool DOT>
 __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) {
   constexpr bool QUAD = ITERS == 0;
   constexpr int NCH = QUAD ? 4 : ITERS;  // 8-element chunks per lane
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[kMaxABytes];
-  __shared__ int32_t part[kWaves][16][16];
+  __shared__ int32_t part[DOT ? 1 : kWaves][16][16];
   __shared__ float bmin[kMaxBlocks], bmax[kMaxBlocks];
   __shared__ float rmin[kWaves], rmax[kWaves];
   __shared__ float rsx[kWaves];
@@ -114,13 +128,18 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
 
   // ---- 1b. the weight stripe, issued right after the activation loads (a
   // wave's loads complete in issue order, so the activations are not queued
-  // behind the weights): lane (r, grp) holds 16 bytes of row n0 + r at
-  // byte 16 * grp of each of the wave's 64-byte blocks.
+  // behind the weights).  MFMA form: lane (r, grp) holds 16 bytes of row
+  // n0 + r at byte 16 * grp of each of the wave's 64-byte blocks.  DOT form:
+  // wave w owns columns n0 + 2w and n0 + 2w + 1, lanes 0-31 the first, 32-63
+  // the second; lane s of a half holds the 16-byte pieces at bytes
+  // 512 i + 16 s, so each load instruction reads two 512-byte runs.
   const int64_t nkb = (d.KB + 63) / 64;
   const int64_t per = (nkb + kWaves - 1) / kWaves;
   const int64_t b0 = wave * per;
-  const uint8_t* brow = d.b + min(n0 + r, d.brows - 1) * d.KB;
   const int64_t off = grp * 16;
+  const int half = lane >> 5, s16 = (lane & 31) * 16;
+  const int64_t dcol = n0 + 2 * wave + half;
+  const uint8_t* brow = d.b + min(DOT ? dcol : n0 + r, d.brows - 1) * d.KB;
   // Pieces past the wave's blocks or the row end (the last block of a row
   // with KB % 64 == 32 is half empty) re-read the row's last piece and are
   // zeroed where they are used: overwriting a load's destination here would
@@ -128,13 +147,19 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
   uint4 bv[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const int64_t kb = (b0 + i) * 64;
-    const bool in = i < per && kb + off < d.KB;
-    bv[i] = *reinterpret_cast<const uint4*>(brow + (in ? kb + off : d.KB - 16));
+    if constexpr (DOT) {
+      const int64_t kb = (int64_t)i * 512 + s16;
+      bv[i] = *reinterpret_cast<const uint4*>(brow + (kb < d.KB ? kb : d.KB - 16));
+    } else {
+      const int64_t kb = (b0 + i) * 64;
+      const bool in = i < per && kb + off < d.KB;
+      bv[i] = *reinterpret_cast<const uint4*>(brow + (in ? kb + off : d.KB - 16));
+    }
   }
-  // Epilogue operands of column n0 + tid % 16, fetched now by every thread
-  // (index clamped; threads < 256 use them) instead of after the dot products.
-  const int64_t nc = min(n0 + (tid & 15), d.N - 1);
+  // Epilogue operands of this thread's column (MFMA form: n0 + tid % 16, used
+  // by threads < 256; DOT form: the lane's column), fetched now (index
+  // clamped) instead of after the dot products.
+  const int64_t nc = min(DOT ? dcol : n0 + (tid & 15), d.N - 1);
   const float e_sw = d.sw[nc];
   const int32_t e_sum = d.sums[nc];
   const float e_b = BIAS ? (float)static_cast<const OutT*>(d.bias)[nc] : 0.0f;
@@ -270,7 +295,52 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
   }
   __syncthreads();
 
-  // ---- 3. dot products: per 64-byte block two v_mfma_i32_16x16x64_i8 (A row
+  if constexpr (DOT) {
+    // ---- 3 (DOT). per 16-byte piece and row m < M, four v_dot8_i32_i4 of the
+    // activation codes (LDS) with the weight piece; the sums over each 32-lane
+    // half (DPP within 16-lane rows, two readlanes); the epilogue of output
+    // (m, column) by lane 32 half + m.  The sums are the reference's raw
+    // values: the nibbles are multiplied as they are.
+    int32_t mine = 0;
+#pragma unroll
+    for (int m = 0; m < kDotMaxRows; ++m) {
+      if (m < d.M) {
+        int32_t acc = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int64_t kb = (int64_t)i * 512 + s16;
+          if (kb < d.KB) {
+            const uint4 av = *reinterpret_cast<const uint4*>(a_lds + m * d.KB + kb);
+            const uint4 bw = bv[i];
+            acc = __builtin_amdgcn_sdot8((int)av.x, (int)bw.x, acc, false);
+            acc = __builtin_amdgcn_sdot8((int)av.y, (int)bw.y, acc, false);
+            acc = __builtin_amdgcn_sdot8((int)av.z, (int)bw.z, acc, false);
+            acc = __builtin_amdgcn_sdot8((int)av.w, (int)bw.w, acc, false);
+          }
+        }
+        acc += __builtin_amdgcn_mov_dpp(acc, kDppQuadXor1, 0xF, 0xF, false);
+        acc += __builtin_amdgcn_mov_dpp(acc, kDppQuadXor2, 0xF, 0xF, false);
+        acc += __builtin_amdgcn_mov_dpp(acc, kDppRowRor4, 0xF, 0xF, false);
+        acc += __builtin_amdgcn_mov_dpp(acc, kDppRowRor8, 0xF, 0xF, false);
+        const int32_t s0 =
+            __builtin_amdgcn_readlane(acc, 0) + __builtin_amdgcn_readlane(acc, 16);
+        const int32_t s1 =
+            __builtin_amdgcn_readlane(acc, 32) + __builtin_amdgcn_readlane(acc, 48);
+        if ((lane & 31) == m) mine = half ? s1 : s0;
+      }
+    }
+    const int ml = lane & 31;
+    if (ml >= d.M || dcol >= d.N) return;
+    // Operation order of kernel/w4a4.cu:74-77.
+    const int32_t corrected = mine + (8 - rzx[ml]) * e_sum;
+    float res = (float)corrected * rsx[ml];
+    res = res * e_sw;
+    if (BIAS) res = res + e_b;
+    static_cast<OutT*>(d.out)[ml * d.N + dcol] = to_out<OutT>(res);
+    return;
+  }
+
+  // ---- 3 (MFMA). per 64-byte block two v_mfma_i32_16x16x64_i8 (A row
   // lane % 16 from LDS, zero past M; B from registers), as the skinny-M GEMM.
   v4i acc = {0, 0, 0, 0};
   const bool arow_live = r < d.M;
@@ -319,7 +389,7 @@ bool linear_decode_fits(int64_t M, int64_t K) {
   const int64_t KP = ceil_to(K, 64), KB = KP / 2;
   const int64_t nblk = (KP + 127) / 128;
   return M >= 1 && M <= kWaves && K % 8 == 0 && M * nblk <= kMaxBlocks && M * KB <= kMaxABytes &&
-         (KB + 63) / 64 <= (int64_t)kWaves * kMaxBlocksPerWave;
+         (KB + 63) / 64 <= (int64_t)kWaves * kMaxBlocksPerWave && (KB + 511) / 512 <= kMaxPieces;
 }
 
 int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, int rotate_block,
@@ -342,16 +412,23 @@ int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, in
   d.out = out;
   const dim3 grid((unsigned)((N + 15) / 16)), block(kWaves * 64);
   const bool rot = rotate_block != 0;
-  const int64_t per = ((d.KB + 63) / 64 + kWaves - 1) / kWaves;
+  const bool dot = M <= kDotMaxRows;
+  const int64_t per = dot ? (d.KB + 511) / 512 : ((d.KB + 63) / 64 + kWaves - 1) / kWaves;
   // 16-lane blocks for up to two passes of 32 blocks, quads beyond.
   const int64_t iters = (M * d.nblk + 31) / 32;
-#define DSCQ_DEC_I(T, O, R, B, P)                                                              \
-  if (iters <= 1)                                                                              \
-    launch((w4a4_decode_kernel<T, O, R, B, P, 1>), grid, block, stream, d);    \
-  else if (iters <= 2)                                                                         \
-    launch((w4a4_decode_kernel<T, O, R, B, P, 2>), grid, block, stream, d);    \
+#define DSCQ_DEC_D(T, O, R, B, P, I)                                                           \
+  if (dot)                                                                                     \
+    launch((w4a4_decode_kernel<T, O, R, B, P, I, true>), grid, block, stream, d);              \
   else                                                                                         \
-    launch((w4a4_decode_kernel<T, O, R, B, P, 0>), grid, block, stream, d);
+    launch((w4a4_decode_kernel<T, O, R, B, P, I, false>), grid, block, stream, d);
+#define DSCQ_DEC_I(T, O, R, B, P)                                                              \
+  if (iters <= 1) {                                                                            \
+    DSCQ_DEC_D(T, O, R, B, P, 1)                                                               \
+  } else if (iters <= 2) {                                                                     \
+    DSCQ_DEC_D(T, O, R, B, P, 2)                                                               \
+  } else {                                                                                     \
+    DSCQ_DEC_D(T, O, R, B, P, 0)                                                               \
+  }
 #define DSCQ_DEC(T, O, R, B)                                                                   \
   if (per <= 4) {                                                                              \
     DSCQ_DEC_I(T, O, R, B, 4)                                                                  \
@@ -376,6 +453,7 @@ int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, in
 #undef DSCQ_DEC_B
 #undef DSCQ_DEC
 #undef DSCQ_DEC_I
+#undef DSCQ_DEC_D
   return launch_status("w4a4_decode_kernel");
 }
 

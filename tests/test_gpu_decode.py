@@ -4,7 +4,7 @@ The fused kernel quantizes the few activation rows inside every workgroup and
 multiplies them with its weight stripe in the same launch.  Its output must
 equal, bit for bit, the two-launch path (quantize, then matmul) and the
 oracle's whole linear (quantize_rows -> gemm_raw -> restore), at the decode
-shapes (M <= 4, K = 4096; M = 1 up to K = 11008) and at the edges: K not a
+shapes (M <= 4, K = 4096; M = 1 up to K = 12288) and at the edges: K not a
 multiple of 128 (no rotation), KB % 64 == 32 (a half-empty last k block),
 N not a multiple of 16, clip < 1 (clamped codes), fp32 input and output,
 bias, and rows that are all zero, constant, or hold exact rounding ties.
@@ -31,6 +31,10 @@ CASES = [
     (2, 192, 40, 0, 0.5, torch.float16, False, False),
     (1, 64, 8, 0, 1.0, torch.float16, False, False),
     (4, 2048, 24, 128, 1.0, torch.float32, False, False),
+    # M <= 2 (the v_dot8 form): the longest row (K = 12288, twelve 16-byte weight
+    # pieces per lane), and fp32 in / out with bias at N = 11008
+    (1, 12288, 520, 128, 1.0, torch.float16, True, False),
+    (2, 4096, 11008, 128, 1.0, torch.float32, True, True),
 ]
 
 

@@ -44,6 +44,12 @@ QUANT_CASES = [
     (4100, 2048, np.float16, 0, 0.75, True),
     (2048, 4096, np.float32, 128, 1.0, True),
     (4096, 8192, np.float16, 128, 1.0, True),
+    # one row per workgroup (two waves per row, MP >= 2048): every row fit,
+    # with and without the clamp
+    (2048, 4096, np.float16, 0, 0.6, True),
+    (2048, 3968, np.float16, 128, 0.8, True),
+    (2048, 3968, np.float16, 0, 1.0, True),
+    (2050, 4000, np.float32, 0, 1.0, True),
     # clip, dtype, two-pass
     (100, 4096, np.float16, 128, 0.5, True),
     (100, 4096, np.float16, 0, 0.75, False),

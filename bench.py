@@ -244,6 +244,14 @@ def counter_summary(counter_csv, workload):
                         (32 busy cycles per v_mfma_i32_32x32x32_i8 on this chip)
       valu_per_element = (SQ_INSTS_VALU - SQ_INSTS_MFMA) * 64 / (M * K): VALU
                         instructions per activation element and lane (quantize).
+    With the wave-state counters (summed over waves, same unit as SQ_WAVE_CYCLES):
+      wait_frac       = SQ_WAIT_ANY / SQ_WAVE_CYCLES, the share of the waves' lifetime
+                        spent in s_waitcnt / barriers (memory and LDS waits)
+      wait_inst_frac  = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES, waiting to issue (dependencies)
+      active_frac     = SQ_ACTIVE_INST_ANY / SQ_WAVE_CYCLES, issuing
+      valu_busy_frac  = 4 * SQ_ACTIVE_INST_VALU / (SIMDs * kernel cycles), the share of
+                        the kernel's cycles a SIMD issues VALU work (a wave64 VALU
+                        instruction occupies the SIMD for 4 cycles).
     """
     import csv
     agent = os.path.join(os.path.dirname(counter_csv),
@@ -273,6 +281,14 @@ def counter_summary(counter_csv, workload):
             entry["clock_ghz"] = round(cycles / d_ns, 3)
             if mean.get("SQ_VALU_MFMA_BUSY_CYCLES"):
                 entry["mfma_busy_frac"] = round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * cycles), 4)
+        waves = mean.get("SQ_WAVE_CYCLES")
+        if waves:
+            for key, name in (("wait_frac", "SQ_WAIT_ANY"), ("wait_inst_frac", "SQ_WAIT_INST_ANY"),
+                              ("active_frac", "SQ_ACTIVE_INST_ANY")):
+                if name in mean:
+                    entry[key] = round(mean[name] / waves, 4)
+        if busy and "SQ_ACTIVE_INST_VALU" in mean:
+            entry["valu_busy_frac"] = round(4 * mean["SQ_ACTIVE_INST_VALU"] / (simds * busy / arrays), 4)
         if cls == "quantize" and "SQ_INSTS_VALU" in mean:
             entry["valu_per_element"] = round(
                 (mean["SQ_INSTS_VALU"] - mean.get("SQ_INSTS_MFMA", 0.0)) * 64 / (M * K), 2)

@@ -135,7 +135,11 @@ def test_counter_summary_formulas(tmp_path):
         rows += [dict(Dispatch_Id=2 * d + 1, Kernel_Name=quant, Counter_Name=c, Counter_Value=v,
                       Start_Timestamp=0, End_Timestamp=8000)
                  for c, v in (("SQ_BUSY_CYCLES", 32 * 16000), ("SQ_INSTS_VALU", 2097152),
-                              ("SQ_INSTS_MFMA", 0))]
+                              ("SQ_INSTS_MFMA", 0), ("SQ_WAVE_CYCLES", 1000000),
+                              ("SQ_WAIT_ANY", 700000), ("SQ_WAIT_INST_ANY", 150000),
+                              ("SQ_ACTIVE_INST_ANY", 150000),
+                              # 1024 SIMDs x 16,000 cycles, a quarter of them issuing VALU
+                              ("SQ_ACTIVE_INST_VALU", 1024 * 16000 // 16))]
     path = tmp_path / "p_counter_collection.csv"
     with open(path, "w", newline="") as f:
         w = csv.DictWriter(f, fieldnames=fields)
@@ -150,3 +154,6 @@ def test_counter_summary_formulas(tmp_path):
     assert s["gemm"]["dispatches"] == 2 and s["gemm"]["clock_ghz"] == 2.0
     assert s["gemm"]["mfma_busy_frac"] == 0.6
     assert s["quantize"]["valu_per_element"] == 4.0 * 4 and s["quantize"]["clock_ghz"] == 2.0
+    q = s["quantize"]
+    assert (q["wait_frac"], q["wait_inst_frac"], q["active_frac"]) == (0.7, 0.15, 0.15)
+    assert q["valu_busy_frac"] == 0.25 and "wait_frac" not in s["gemm"]

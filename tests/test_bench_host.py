@@ -89,9 +89,11 @@ def test_committed_traffic_blocks(workload, classes):
         assert t[c]["traffic"] == t[c]["fetch_bytes"] + t[c]["write_bytes"]
     if workload == "prefill":
         M, N, K, _ = bench.WORKLOADS["prefill"]
-        # the GEMM writes exactly its fp16 output; the quantize kernel its packed codes + metadata
+        # the GEMM writes exactly its fp16 output; the quantize kernel its packed codes and
+        # metadata, where each row's 4-byte scale and zero-point may take a 32-byte granule
         assert abs(t["gemm"]["write_bytes"] - 2 * M * N) < 1024
-        assert abs(t["quantize"]["write_bytes"] - (M * K // 2 + 8 * M)) < 64 * 1024
+        extra = t["quantize"]["write_bytes"] - (M * K // 2 + 8 * M)
+        assert 0 <= extra <= 64 * M
 
 
 def test_workloads_are_well_formed():

@@ -361,28 +361,29 @@ __global__ __launch_bounds__(TPB) void row_quant_kernel(RowArgs a) {
   };
   if (a.packed) {
     uint8_t* const prow = a.packed + row * (a.KP / 2);
-    if constexpr (FULL) {
-      // A wave's packed blocks of an iteration (16 x 64 bytes, contiguous in
-      // the row) pass through LDS so that each lane stores 16 contiguous
-      // bytes: one store instruction per iteration instead of four 4-byte
-      // pieces per lane, and whole 64-byte segments leave the CU (M = 2048,
-      // K = 4096: 5.52 -> 4.33 MB written, 7.57 -> 7.45 us).  A wave reads back
-      // only what it wrote; its LDS accesses complete in order.
-      __shared__ uint32_t pstage[TPB / 64][ITERS][256];
+    // A wave's packed blocks of an iteration (16 x 64 bytes, contiguous in the
+    // row) pass through LDS so that each lane stores 16 contiguous bytes (32
+    // elements; KP is a multiple of 64, so a piece is wholly inside or past
+    // it): one store instruction per iteration instead of four 4-byte pieces
+    // per lane, and whole 64-byte segments leave the CU.  Measured: M = 2048,
+    // K = 4096 5.52 -> 4.33 MB written, 7.57 -> 7.45 us; 4096 x 28672 59.5 ->
+    // 55.4 us.  A wave reads back only what it wrote; its LDS accesses
+    // complete in order.
+    __shared__ uint32_t pstage[TPB / 64][ITERS][256];
 #pragma unroll
-      for (int it = 0; it < ITERS; ++it)
+    for (int it = 0; it < ITERS; ++it) {
+      if (!FULL && !(wlive[it] || !real)) continue;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          pstage[wave][it][(lane >> 2) * 16 + j * 4 + r] = packed_nibbles(ev[it][j], od[it][j]);
+      for (int j = 0; j < 4; ++j)
+        pstage[wave][it][(lane >> 2) * 16 + j * 4 + r] = packed_nibbles(ev[it][j], od[it][j]);
+    }
 #pragma unroll
-      for (int it = 0; it < ITERS; ++it) {
-        const uint4 v = *reinterpret_cast<const uint4*>(&pstage[wave][it][lane * 4]);
-        store_stream(v, prow + (uint32_t)((wave_in_row * 16 + it * NQ) * 64 + lane * 16));
-      }
-    } else {
-      store_iters([&](int it, int j, int e0) {
-        store_stream(packed_nibbles(ev[it][j], od[it][j]), prow + (uint32_t)e0 / 2u);
-      });
+    for (int it = 0; it < ITERS; ++it) {
+      if (!FULL && !(wlive[it] || !real)) continue;
+      const int b = wave_in_row * 16 + it * NQ + (lane >> 2);
+      const int pe0 = b * 128 + (lane & 3) * 32;
+      const uint4 v = *reinterpret_cast<const uint4*>(&pstage[wave][it][lane * 4]);
+      if (FULL || (b < a.nblk && (WHOLE || pe0 < a.KP))) store_stream(v, prow + (uint32_t)pe0 / 2u);
     }
   }
   if (a.codes)

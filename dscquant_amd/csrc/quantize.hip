@@ -18,8 +18,10 @@
 // in-register stages, and a load instruction of the wave reads 16 quads x 64
 // contiguous bytes.  A row is spread over WPR waves (16*WPR quads), each quad
 // taking blocks quad, quad + 16*WPR, ... up to ITERS of them; the whole row
-// stays in VGPRs, so x is read from HBM exactly once.  Rows longer than the
-// register capacity use the two-pass streaming kernel at the end.
+// stays in VGPRs, so x is read from HBM exactly once.  The packed codes of a
+// wave's 16 blocks pass through LDS on the way out, so that each lane stores
+// 16 contiguous bytes.  Rows longer than the register capacity use the
+// two-pass streaming kernel at the end.
 //
 // The per-element rules and the exactness argument of the fast division are
 // in rowquant.h.

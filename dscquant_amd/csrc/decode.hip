@@ -15,6 +15,9 @@
 //      (kernel/w4a4.cu:70-78, 156-161).  Two forms:
 //        MFMA (M >= 3): int8 MFMAs over the unpacked nibbles, the 16 columns
 //          as one 16 x 16 tile, each wave on a K range, sums meeting in LDS;
+//          where the grid would take up to three rounds over the CUs, a
+//          workgroup owns two or three such tiles (the activation fragment
+//          unpacked once for all of them) and quantizes once for them all;
 //        DOT (M <= 2): v_dot8_i32_i4 (eight signed-nibble products per
 //          instruction, straight on the packed bytes: both operands already
 //          hold two's-complement nibbles, (q - 8) & 15 and c & 15), each wave
@@ -31,6 +34,7 @@
 // Result: out == matmul(quantize(x, clip, fused, rotate_block), b, ...) of
 // the reference extension (kernel/w4a4.cu:164-225), bit for bit.
 
+#include <algorithm>
 #include <cstdlib>
 
 #include "../../include/dscq.h"
@@ -93,19 +97,20 @@ __device__ __forceinline__ void bfly_swizzle(float (&c)[8], float sgn) {
 //     (pairs share r, hence the sign).  8 elements per lane per pass.
 //   QUAD (ITERS = 0, M * nblk <= 128): the quantize kernel's layout, a block
 //     per quad of lanes, 32 elements per lane, bits 5-6 in the lane.
-template <typename T, typename OutT, bool ROT, bool BIAS, int PER, int ITERS, bool DOT>
+template <typename T, typename OutT, bool ROT, bool BIAS, int PER, int ITERS, bool DOT, int NT>
 __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) {
   constexpr bool QUAD = ITERS == 0;
   constexpr int NCH = QUAD ? 4 : ITERS;  // 8-element chunks per lane
+  static_assert(!DOT || NT == 1, "the v_dot8 form owns 16 columns per workgroup");
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[kMaxABytes];
-  __shared__ int32_t part[DOT ? 1 : kWaves][16][16];
+  __shared__ int32_t part[DOT ? 1 : kWaves][NT][16][16];
   __shared__ float bmin[kMaxBlocks], bmax[kMaxBlocks];
   __shared__ float rmin[kWaves], rmax[kWaves];
   __shared__ float rsx[kWaves];
   __shared__ int32_t rzx[kWaves];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t n0 = (int64_t)blockIdx.x * 16 * NT;
   const int r = lane & 15, grp = lane >> 4;
 
   // ---- 1a. activations.  Chunk c of this lane: block slot g[c] (row
@@ -139,30 +144,38 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
   const int64_t off = grp * 16;
   const int half = lane >> 5, s16 = (lane & 31) * 16;
   const int64_t dcol = n0 + 2 * wave + half;
-  const uint8_t* brow = d.b + min(DOT ? dcol : n0 + r, d.brows - 1) * d.KB;
   // Pieces past the wave's blocks or the row end (the last block of a row
   // with KB % 64 == 32 is half empty) re-read the row's last piece and are
   // zeroed where they are used: overwriting a load's destination here would
-  // wait for the load.
-  uint4 bv[PER];
+  // wait for the load.  MFMA form: NT tiles of 16 columns, n0 + 16 t + r.
+  uint4 bv[NT][PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    if constexpr (DOT) {
-      const int64_t kb = (int64_t)i * 512 + s16;
-      bv[i] = *reinterpret_cast<const uint4*>(brow + (kb < d.KB ? kb : d.KB - 16));
-    } else {
-      const int64_t kb = (b0 + i) * 64;
-      const bool in = i < per && kb + off < d.KB;
-      bv[i] = *reinterpret_cast<const uint4*>(brow + (in ? kb + off : d.KB - 16));
+  for (int t = 0; t < NT; ++t) {
+    const uint8_t* brow = d.b + min(DOT ? dcol : n0 + 16 * t + r, d.brows - 1) * d.KB;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if constexpr (DOT) {
+        const int64_t kb = (int64_t)i * 512 + s16;
+        bv[t][i] = *reinterpret_cast<const uint4*>(brow + (kb < d.KB ? kb : d.KB - 16));
+      } else {
+        const int64_t kb = (b0 + i) * 64;
+        const bool in = i < per && kb + off < d.KB;
+        bv[t][i] = *reinterpret_cast<const uint4*>(brow + (in ? kb + off : d.KB - 16));
+      }
     }
   }
-  // Epilogue operands of this thread's column (MFMA form: n0 + tid % 16, used
-  // by threads < 256; DOT form: the lane's column), fetched now (index
-  // clamped) instead of after the dot products.
-  const int64_t nc = min(DOT ? dcol : n0 + (tid & 15), d.N - 1);
-  const float e_sw = d.sw[nc];
-  const int32_t e_sum = d.sums[nc];
-  const float e_b = BIAS ? (float)static_cast<const OutT*>(d.bias)[nc] : 0.0f;
+  // Epilogue operands of this thread's columns (MFMA form: n0 + 16 t + tid %
+  // 16, used by threads < 256; DOT form: the lane's column), fetched now
+  // (index clamped) instead of after the dot products.
+  float e_sw[NT], e_b[NT];
+  int32_t e_sum[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int64_t nc = min(DOT ? dcol : n0 + 16 * t + (tid & 15), d.N - 1);
+    e_sw[t] = d.sw[nc];
+    e_sum[t] = d.sums[nc];
+    e_b[t] = BIAS ? (float)static_cast<const OutT*>(d.bias)[nc] : 0.0f;
+  }
   // Keep every load above the arithmetic (the scheduler would otherwise sink
   // the weight loads below the transform to save registers).
   __builtin_amdgcn_sched_barrier(0);
@@ -311,7 +324,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
           const int64_t kb = (int64_t)i * 512 + s16;
           if (kb < d.KB) {
             const uint4 av = *reinterpret_cast<const uint4*>(a_lds + m * d.KB + kb);
-            const uint4 bw = bv[i];
+            const uint4 bw = bv[0][i];
             acc = __builtin_amdgcn_sdot8((int)av.x, (int)bw.x, acc, false);
             acc = __builtin_amdgcn_sdot8((int)av.y, (int)bw.y, acc, false);
             acc = __builtin_amdgcn_sdot8((int)av.z, (int)bw.z, acc, false);
@@ -332,17 +345,20 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
     const int ml = lane & 31;
     if (ml >= d.M || dcol >= d.N) return;
     // Operation order of kernel/w4a4.cu:74-77.
-    const int32_t corrected = mine + (8 - rzx[ml]) * e_sum;
+    const int32_t corrected = mine + (8 - rzx[ml]) * e_sum[0];
     float res = (float)corrected * rsx[ml];
-    res = res * e_sw;
-    if (BIAS) res = res + e_b;
+    res = res * e_sw[0];
+    if (BIAS) res = res + e_b[0];
     static_cast<OutT*>(d.out)[ml * d.N + dcol] = to_out<OutT>(res);
     return;
   }
 
-  // ---- 3 (MFMA). per 64-byte block two v_mfma_i32_16x16x64_i8 (A row
-  // lane % 16 from LDS, zero past M; B from registers), as the skinny-M GEMM.
-  v4i acc = {0, 0, 0, 0};
+  // ---- 3 (MFMA). per 64-byte block two v_mfma_i32_16x16x64_i8 per column
+  // tile (A row lane % 16 from LDS, zero past M, shared by the tiles; B from
+  // registers), as the skinny-M GEMM.
+  v4i acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
   const bool arow_live = r < d.M;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -351,34 +367,42 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
       const bool in = kb + off < d.KB;
       uint4 av = make_uint4(0u, 0u, 0u, 0u);
       if (arow_live && in) av = *reinterpret_cast<const uint4*>(a_lds + r * d.KB + kb + off);
-      uint4 bw = bv[i];
-      bw.x = in ? bw.x : 0u;
-      bw.y = in ? bw.y : 0u;
-      bw.z = in ? bw.z : 0u;
-      bw.w = in ? bw.w : 0u;
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(av.x, av.y), unpack8(bw.x, bw.y),
-                                                  acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack8(av.z, av.w), unpack8(bw.z, bw.w),
-                                                  acc, 0, 0, 0);
+      const v4i a_lo = unpack8(av.x, av.y), a_hi = unpack8(av.z, av.w);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        uint4 bw = bv[t][i];
+        bw.x = in ? bw.x : 0u;
+        bw.y = in ? bw.y : 0u;
+        bw.z = in ? bw.z : 0u;
+        bw.w = in ? bw.w : 0u;
+        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_lo, unpack8(bw.x, bw.y), acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_hi, unpack8(bw.z, bw.w), acc[t], 0, 0, 0);
+      }
     }
   }
   // D of a 16 x 16 tile: row (A) 4 * (lane / 16) + v, column (B) lane % 16.
 #pragma unroll
-  for (int t = 0; t < 4; ++t) part[wave][4 * grp + t][r] = acc[t] >> 8;
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[wave][t][4 * grp + v][r] = acc[t][v] >> 8;
   __syncthreads();
   if (tid >= 256) return;
   const int ml = tid >> 4, nl = tid & 15;
-  const int64_t m = ml, n = n0 + nl;
-  if (m >= d.M || n >= d.N) return;
-  int32_t rawv = 0;
+  if (ml >= d.M) return;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) rawv += part[w][ml][nl];
-  // Operation order of kernel/w4a4.cu:74-77.
-  const int32_t corrected = rawv + (8 - rzx[ml]) * e_sum;
-  float res = (float)corrected * rsx[ml];
-  res = res * e_sw;
-  if (BIAS) res = res + e_b;
-  static_cast<OutT*>(d.out)[m * d.N + n] = to_out<OutT>(res);
+  for (int t = 0; t < NT; ++t) {
+    const int64_t n = n0 + 16 * t + nl;
+    if (n >= d.N) break;
+    int32_t rawv = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) rawv += part[w][t][ml][nl];
+    // Operation order of kernel/w4a4.cu:74-77.
+    const int32_t corrected = rawv + (8 - rzx[ml]) * e_sum[t];
+    float res = (float)corrected * rsx[ml];
+    res = res * e_sw[t];
+    if (BIAS) res = res + e_b[t];
+    static_cast<OutT*>(d.out)[ml * d.N + n] = to_out<OutT>(res);
+  }
 }
 
 }  // namespace
@@ -410,17 +434,32 @@ int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, in
   d.bias = bias;
   d.N = N;
   d.out = out;
-  const dim3 grid((unsigned)((N + 15) / 16)), block(kWaves * 64);
   const bool rot = rotate_block != 0;
   const bool dot = M <= kDotMaxRows;
+  // MFMA form: a workgroup takes NT tiles of 16 columns, since every
+  // workgroup re-quantizes all M rows.  Up to three tiles per CU, NT spreads
+  // them in one round (M = 4 graph-replayed, weights from HBM, one tile /
+  // NT: N = 8192 8.2 / 7.3 us, N = 11008 10.3 / 8.5, N = 12288 10.5 / 8.8);
+  // past that, two tiles per workgroup (N = 14336 12.5 / 10.2, N = 28672
+  // 21.2 / 16.6): three would leave a short second round (14.4 and 21.0 us).
+  const int64_t tiles = (N + 15) / 16, cus = cu_count();
+  const int64_t per_cu = (tiles + cus - 1) / cus;
+  const int nt = dot ? 1 : per_cu > 3 ? 2 : (int)std::max<int64_t>(1, per_cu);
+  const dim3 grid((unsigned)((tiles + nt - 1) / nt)), block(kWaves * 64);
   const int64_t per = dot ? (d.KB + 511) / 512 : ((d.KB + 63) / 64 + kWaves - 1) / kWaves;
   // 16-lane blocks for up to two passes of 32 blocks, quads beyond.
   const int64_t iters = (M * d.nblk + 31) / 32;
+  // (The MFMA form needs M >= 3, so M * ceil(K / 128) <= 128 keeps its K at
+  // most 5376 and its weight pieces at most 8: no twelve-piece MFMA kernels.)
 #define DSCQ_DEC_D(T, O, R, B, P, I)                                                           \
-  if (dot)                                                                                     \
-    launch((w4a4_decode_kernel<T, O, R, B, P, I, true>), grid, block, stream, d);              \
+  if (dot || P == 12)                                                                          \
+    launch((w4a4_decode_kernel<T, O, R, B, P, I, true, 1>), grid, block, stream, d);           \
+  else if (nt == 1)                                                                            \
+    launch((w4a4_decode_kernel<T, O, R, B, P, I, false, 1>), grid, block, stream, d);          \
+  else if (nt == 2)                                                                            \
+    launch((w4a4_decode_kernel<T, O, R, B, P, I, false, 2>), grid, block, stream, d);          \
   else                                                                                         \
-    launch((w4a4_decode_kernel<T, O, R, B, P, I, false>), grid, block, stream, d);
+    launch((w4a4_decode_kernel<T, O, R, B, P, I, false, 3>), grid, block, stream, d);
 #define DSCQ_DEC_I(T, O, R, B, P)                                                              \
   if (iters <= 1) {                                                                            \
     DSCQ_DEC_D(T, O, R, B, P, 1)                                                               \

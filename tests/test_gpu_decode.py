@@ -35,6 +35,13 @@ CASES = [
     # pieces per lane), and fp32 in / out with bias at N = 11008
     (1, 12288, 520, 128, 1.0, torch.float16, True, False),
     (2, 4096, 11008, 128, 1.0, torch.float32, True, True),
+    # M >= 3 with two or three 16-column tiles per workgroup (up to three
+    # tiles per CU: N = 11008 three, ragged N = 8200 three with a short last
+    # workgroup, N = 6000 two) and two past that (N = 14336)
+    (4, 4096, 11008, 128, 1.0, torch.float16, True, False),
+    (3, 5376, 8200, 0, 0.9, torch.float16, False, True),
+    (4, 2048, 6000, 128, 1.0, torch.float32, True, False),
+    (4, 4096, 14336, 128, 0.8, torch.float16, False, False),
 ]
 
 

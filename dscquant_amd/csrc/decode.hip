@@ -15,13 +15,13 @@
 //      (kernel/w4a4.cu:70-78, 156-161).  Two forms:
 //        MFMA (M >= 3): int8 MFMAs over the unpacked nibbles, the 16 columns
 //          as one 16 x 16 tile, each wave on a K range, sums meeting in LDS;
-//          where the grid would take up to three rounds over the CUs, a
-//          workgroup owns two or three such tiles (the activation fragment
-//          unpacked once for all of them) and quantizes once for them all;
 //        DOT (M <= 2): v_dot8_i32_i4 (eight signed-nibble products per
 //          instruction, straight on the packed bytes: both operands already
 //          hold two's-complement nibbles, (q - 8) & 15 and c & 15), each wave
 //          on two of the 16 columns over all of K, so no sums cross waves.
+//      Where the grid would take two or more rounds over the CUs, a workgroup
+//      owns two or three such 16-column tiles (the activation fragment read
+//      and unpacked once for all of them), so it quantizes once for them all.
 //          Measured against MFMA (graph-replayed, weights from HBM, identical
 //          outputs): M = 1, K = N = 4096 4.70 / 4.72 us; M = 1, N = 11008
 //          6.87 / 7.50 us; M = 1, K = 11008 7.36 / 9.20 us; M = 2 5.58 /
@@ -101,7 +101,6 @@ template <typename T, typename OutT, bool ROT, bool BIAS, int PER, int ITERS, bo
 __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) {
   constexpr bool QUAD = ITERS == 0;
   constexpr int NCH = QUAD ? 4 : ITERS;  // 8-element chunks per lane
-  static_assert(!DOT || NT == 1, "the v_dot8 form owns 16 columns per workgroup");
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[kMaxABytes];
   __shared__ int32_t part[DOT ? 1 : kWaves][NT][16][16];
   __shared__ float bmin[kMaxBlocks], bmax[kMaxBlocks];
@@ -143,7 +142,8 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
   const int64_t b0 = wave * per;
   const int64_t off = grp * 16;
   const int half = lane >> 5, s16 = (lane & 31) * 16;
-  const int64_t dcol = n0 + 2 * wave + half;
+  // DOT form: the lane's column of tile t.
+  auto dcol = [&](int t) { return n0 + 16 * t + 2 * wave + half; };
   // Pieces past the wave's blocks or the row end (the last block of a row
   // with KB % 64 == 32 is half empty) re-read the row's last piece and are
   // zeroed where they are used: overwriting a load's destination here would
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
   uint4 bv[NT][PER];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const uint8_t* brow = d.b + min(DOT ? dcol : n0 + 16 * t + r, d.brows - 1) * d.KB;
+    const uint8_t* brow = d.b + min(DOT ? dcol(t) : n0 + 16 * t + r, d.brows - 1) * d.KB;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       if constexpr (DOT) {
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
   int32_t e_sum[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const int64_t nc = min(DOT ? dcol : n0 + 16 * t + (tid & 15), d.N - 1);
+    const int64_t nc = min(DOT ? dcol(t) : n0 + 16 * t + (tid & 15), d.N - 1);
     e_sw[t] = d.sw[nc];
     e_sum[t] = d.sums[nc];
     e_b[t] = BIAS ? (float)static_cast<const OutT*>(d.bias)[nc] : 0.0f;
@@ -314,42 +314,56 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
     // half (DPP within 16-lane rows, two readlanes); the epilogue of output
     // (m, column) by lane 32 half + m.  The sums are the reference's raw
     // values: the nibbles are multiplied as they are.
-    int32_t mine = 0;
+    int32_t mine[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) mine[t] = 0;
 #pragma unroll
     for (int m = 0; m < kDotMaxRows; ++m) {
       if (m < d.M) {
-        int32_t acc = 0;
+        int32_t acc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = 0;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
           const int64_t kb = (int64_t)i * 512 + s16;
           if (kb < d.KB) {
             const uint4 av = *reinterpret_cast<const uint4*>(a_lds + m * d.KB + kb);
-            const uint4 bw = bv[0][i];
-            acc = __builtin_amdgcn_sdot8((int)av.x, (int)bw.x, acc, false);
-            acc = __builtin_amdgcn_sdot8((int)av.y, (int)bw.y, acc, false);
-            acc = __builtin_amdgcn_sdot8((int)av.z, (int)bw.z, acc, false);
-            acc = __builtin_amdgcn_sdot8((int)av.w, (int)bw.w, acc, false);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+              const uint4 bw = bv[t][i];
+              acc[t] = __builtin_amdgcn_sdot8((int)av.x, (int)bw.x, acc[t], false);
+              acc[t] = __builtin_amdgcn_sdot8((int)av.y, (int)bw.y, acc[t], false);
+              acc[t] = __builtin_amdgcn_sdot8((int)av.z, (int)bw.z, acc[t], false);
+              acc[t] = __builtin_amdgcn_sdot8((int)av.w, (int)bw.w, acc[t], false);
+            }
           }
         }
-        acc += __builtin_amdgcn_mov_dpp(acc, kDppQuadXor1, 0xF, 0xF, false);
-        acc += __builtin_amdgcn_mov_dpp(acc, kDppQuadXor2, 0xF, 0xF, false);
-        acc += __builtin_amdgcn_mov_dpp(acc, kDppRowRor4, 0xF, 0xF, false);
-        acc += __builtin_amdgcn_mov_dpp(acc, kDppRowRor8, 0xF, 0xF, false);
-        const int32_t s0 =
-            __builtin_amdgcn_readlane(acc, 0) + __builtin_amdgcn_readlane(acc, 16);
-        const int32_t s1 =
-            __builtin_amdgcn_readlane(acc, 32) + __builtin_amdgcn_readlane(acc, 48);
-        if ((lane & 31) == m) mine = half ? s1 : s0;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          int32_t a = acc[t];
+          a += __builtin_amdgcn_mov_dpp(a, kDppQuadXor1, 0xF, 0xF, false);
+          a += __builtin_amdgcn_mov_dpp(a, kDppQuadXor2, 0xF, 0xF, false);
+          a += __builtin_amdgcn_mov_dpp(a, kDppRowRor4, 0xF, 0xF, false);
+          a += __builtin_amdgcn_mov_dpp(a, kDppRowRor8, 0xF, 0xF, false);
+          const int32_t s0 = __builtin_amdgcn_readlane(a, 0) + __builtin_amdgcn_readlane(a, 16);
+          const int32_t s1 = __builtin_amdgcn_readlane(a, 32) + __builtin_amdgcn_readlane(a, 48);
+          if ((lane & 31) == m) mine[t] = half ? s1 : s0;
+        }
       }
     }
     const int ml = lane & 31;
-    if (ml >= d.M || dcol >= d.N) return;
-    // Operation order of kernel/w4a4.cu:74-77.
-    const int32_t corrected = mine + (8 - rzx[ml]) * e_sum[0];
-    float res = (float)corrected * rsx[ml];
-    res = res * e_sw[0];
-    if (BIAS) res = res + e_b[0];
-    static_cast<OutT*>(d.out)[ml * d.N + dcol] = to_out<OutT>(res);
+    if (ml >= d.M) return;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int64_t n = dcol(t);
+      if (n >= d.N) break;
+      // Operation order of kernel/w4a4.cu:74-77.
+      const int32_t corrected = mine[t] + (8 - rzx[ml]) * e_sum[t];
+      float res = (float)corrected * rsx[ml];
+      res = res * e_sw[t];
+      if (BIAS) res = res + e_b[t];
+      static_cast<OutT*>(d.out)[ml * d.N + n] = to_out<OutT>(res);
+    }
     return;
   }
 
@@ -407,6 +421,41 @@ __global__ __launch_bounds__(kWaves * 64) void w4a4_decode_kernel(DecodeArgs d) 
 
 }  // namespace
 
+// One launch of the chosen form and tile count.  The MFMA form needs M >= 3,
+// so M * ceil(K / 128) <= 128 keeps its K at most 5376 and its weight pieces
+// at most 8; the v_dot8 form takes several tiles only with four pieces.
+template <typename T, typename O, bool R, bool B, int P, int I>
+bool launch_decode(bool dot, int nt, dim3 grid, dim3 block, hipStream_t stream,
+                   const DecodeArgs& d) {
+  if (dot) {
+    if constexpr (P <= 4) {
+      if (nt == 2) {
+        launch((w4a4_decode_kernel<T, O, R, B, P, I, true, 2>), grid, block, stream, d);
+        return true;
+      }
+      if (nt == 3) {
+        launch((w4a4_decode_kernel<T, O, R, B, P, I, true, 3>), grid, block, stream, d);
+        return true;
+      }
+    }
+    if (nt != 1) return false;
+    launch((w4a4_decode_kernel<T, O, R, B, P, I, true, 1>), grid, block, stream, d);
+    return true;
+  }
+  if constexpr (P <= 8) {
+    if (nt == 1)
+      launch((w4a4_decode_kernel<T, O, R, B, P, I, false, 1>), grid, block, stream, d);
+    else if (nt == 2)
+      launch((w4a4_decode_kernel<T, O, R, B, P, I, false, 2>), grid, block, stream, d);
+    else if (nt == 3)
+      launch((w4a4_decode_kernel<T, O, R, B, P, I, false, 3>), grid, block, stream, d);
+    else
+      return false;
+    return true;
+  }
+  return false;
+}
+
 // The limits the fused kernel accepts (see the file comment); callers check
 // them with linear_decode_fits and otherwise quantize and multiply separately.
 bool linear_decode_fits(int64_t M, int64_t K) {
@@ -436,30 +485,28 @@ int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, in
   d.out = out;
   const bool rot = rotate_block != 0;
   const bool dot = M <= kDotMaxRows;
-  // MFMA form: a workgroup takes NT tiles of 16 columns, since every
-  // workgroup re-quantizes all M rows.  Up to three tiles per CU, NT spreads
-  // them in one round (M = 4 graph-replayed, weights from HBM, one tile /
-  // NT: N = 8192 8.2 / 7.3 us, N = 11008 10.3 / 8.5, N = 12288 10.5 / 8.8);
-  // past that, two tiles per workgroup (N = 14336 12.5 / 10.2, N = 28672
-  // 21.2 / 16.6): three would leave a short second round (14.4 and 21.0 us).
+  // A workgroup takes NT tiles of 16 columns, since every workgroup
+  // re-quantizes all M rows.  Up to three tiles per CU, NT spreads them in
+  // one round; past that, two tiles per workgroup (three would leave a short
+  // second round).  Graph-replayed, weights from HBM, one tile / NT:
+  //   MFMA form, M = 4, K = 4096: N = 8192 8.2 / 7.3 us, N = 11008 10.3 /
+  //   8.5, N = 12288 10.5 / 8.8, N = 14336 12.5 / 10.2 (three tiles 14.4),
+  //   N = 28672 21.2 / 16.6 (three 21.0);
+  //   v_dot8 form, K = 4096 (four weight pieces per lane): M = 1, N = 8192
+  //   5.91 / 5.56, N = 11008 6.85 / 6.62 (two tiles 6.94), N = 14336 8.25 /
+  //   7.41, N = 28672 12.6 / 12.2; M = 2, N = 11008 8.67 / 7.93.  With eight
+  //   pieces (K = 8192) the extra registers cost more (M = 1, N = 8192 8.8 /
+  //   9.2; M = 2, N = 28672 25.0 / 30.3): one tile.
   const int64_t tiles = (N + 15) / 16, cus = cu_count();
   const int64_t per_cu = (tiles + cus - 1) / cus;
-  const int nt = dot ? 1 : per_cu > 3 ? 2 : (int)std::max<int64_t>(1, per_cu);
-  const dim3 grid((unsigned)((tiles + nt - 1) / nt)), block(kWaves * 64);
   const int64_t per = dot ? (d.KB + 511) / 512 : ((d.KB + 63) / 64 + kWaves - 1) / kWaves;
+  const int nt = (dot && per > 4) ? 1 : per_cu > 3 ? 2 : (int)std::max<int64_t>(1, per_cu);
+  const dim3 grid((unsigned)((tiles + nt - 1) / nt)), block(kWaves * 64);
   // 16-lane blocks for up to two passes of 32 blocks, quads beyond.
   const int64_t iters = (M * d.nblk + 31) / 32;
-  // (The MFMA form needs M >= 3, so M * ceil(K / 128) <= 128 keeps its K at
-  // most 5376 and its weight pieces at most 8: no twelve-piece MFMA kernels.)
-#define DSCQ_DEC_D(T, O, R, B, P, I)                                                           \
-  if (dot || P == 12)                                                                          \
-    launch((w4a4_decode_kernel<T, O, R, B, P, I, true, 1>), grid, block, stream, d);           \
-  else if (nt == 1)                                                                            \
-    launch((w4a4_decode_kernel<T, O, R, B, P, I, false, 1>), grid, block, stream, d);          \
-  else if (nt == 2)                                                                            \
-    launch((w4a4_decode_kernel<T, O, R, B, P, I, false, 2>), grid, block, stream, d);          \
-  else                                                                                         \
-    launch((w4a4_decode_kernel<T, O, R, B, P, I, false, 3>), grid, block, stream, d);
+  bool launched = false;
+#define DSCQ_DEC_D(T, O, R, B, P, I) \
+  launched = launch_decode<T, O, R, B, P, I>(dot, nt, grid, block, stream, d);
 #define DSCQ_DEC_I(T, O, R, B, P)                                                              \
   if (iters <= 1) {                                                                            \
     DSCQ_DEC_D(T, O, R, B, P, 1)                                                               \
@@ -493,6 +540,7 @@ int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, in
 #undef DSCQ_DEC
 #undef DSCQ_DEC_I
 #undef DSCQ_DEC_D
+  if (!launched) return fail("internal: no decode kernel for M=%lld K=%lld tiles=%d", (long long)M, (long long)K, nt);
   return launch_status("w4a4_decode_kernel");
 }
 

@@ -42,6 +42,11 @@ CASES = [
     (3, 5376, 8200, 0, 0.9, torch.float16, False, True),
     (4, 2048, 6000, 128, 1.0, torch.float32, True, False),
     (4, 4096, 14336, 128, 0.8, torch.float16, False, False),
+    # M <= 2 with several tiles per workgroup (up to four weight pieces per
+    # lane): N = 14336 two, ragged N = 8200 three; K = 8192 keeps one (N = 8192)
+    (1, 4096, 14336, 128, 1.0, torch.float16, True, False),
+    (2, 2048, 8200, 0, 0.7, torch.float32, False, True),
+    (1, 8192, 8192, 128, 1.0, torch.float16, False, False),
 ]
 
 

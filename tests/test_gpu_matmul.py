@@ -90,6 +90,13 @@ MM_CASES = [
     # rows with an fp32 bias; N past the last full tile with a K tail)
     (300, 2048, 8192, True, True, False),
     (64, 8200, 4352, True, False, False),
+    # 256 x 128 tiles past one round: two rounds (even slice count), 448
+    # tiles (a 75% last round, odd slice count, fp32 out), a K tail with an
+    # fp32 bias, and a single slice
+    (2048, 8192, 512, True, False, False),
+    (3584, 4096, 4352, False, True, False),
+    (2048, 8192, 4160, True, True, False),
+    (2048, 8192, 256, False, False, False),
 ]
 
 

@@ -66,21 +66,6 @@ struct DecodeArgs {
   void* out;              // [M, N]
 };
 
-// Cross-lane butterfly through the LDS crossbar (ds_swizzle, no memory):
-// partner = lane ^ XOR within 32 lanes; the lane whose XOR bit is clear keeps
-// own + partner, the other partner - own -- fma(+-1, own, partner), rounded
-// exactly like the plain add / subtract.
-template <int XOR>
-__device__ __forceinline__ void bfly_swizzle(float (&c)[8], float sgn) {
-  constexpr int kPattern = 0x1F | (XOR << 10);  // bit mode: and 0x1f, xor XOR
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float p = __builtin_bit_cast(
-        float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, c[i]), kPattern));
-    c[i] = __builtin_fmaf(sgn, c[i], p);
-  }
-}
-
 // PER: weight pieces held per lane -- MFMA form: 64-byte blocks per wave (4,
 // 8 or 12 >= the blocks a wave owns); DOT form: 16-byte pieces of the lane's
 // weight row (4, 8 or 12 >= ceil(KB / 512)) -- a compile-time count so the

@@ -21,7 +21,9 @@
 // stays in VGPRs, so x is read from HBM exactly once.  The packed codes of a
 // wave's 16 blocks pass through LDS on the way out, so that each lane stores
 // 16 contiguous bytes.  Rows longer than the register capacity use the
-// two-pass streaming kernel at the end.
+// two-pass streaming kernel at the end; up to 512 activation rows of at most
+// 32 blocks (decode and small batches) take the few-row kernel, a block over
+// 16 lanes instead of 4.
 //
 // The per-element rules and the exactness argument of the fast division are
 // in rowquant.h.
@@ -37,6 +39,11 @@ namespace dscq {
 namespace {
 
 constexpr int kThreads = 256;
+// Rows up to which activations of at most 32 blocks take the few-row kernel.
+// Graph-replayed, K = 4096 with rotation, identical codes, register kernel /
+// few-row kernel: 1 row 2.63 / 2.28 us, 16 rows 3.05 / 2.50, 64 3.57 / 2.96,
+// 256 3.84 / 3.29, 512 4.30 / 4.08, 1024 5.77 / 5.80.
+constexpr int64_t kSpreadMaxRows = 512;
 
 struct RowArgs {
   const void* x;       // [M, K] T
@@ -508,6 +515,93 @@ __global__ __launch_bounds__(kThreads) void row_quant_stream_kernel(RowArgs a) {
   if (wave == 0 && lane == 0) write_row_meta<MODE>(a, row, real, rs, sum);
 }
 
+// ------------------------------------------------------- few-row kernel
+// Activation rows of at most 32 blocks (K <= 4096) when there are few of
+// them (decode): one row per 512-thread workgroup, a 128-element block over
+// 16 consecutive lanes, lane 4j + r holding elements j*32 + r*8 .. +7 (one
+// 16-byte load) -- 8 elements per lane instead of the register kernel's 32,
+// so each wave's chain of arithmetic is a quarter as long.  The transform
+// runs index bits 0-2 in the lane, bits 3-4 across the quad by DPP
+// (sign-folded as in the register kernel) and bits 5-6 across quads by
+// ds_swizzle xor 4 / xor 8, the same butterflies in the same order, so every
+// value, code, scale and zero-point is the register kernel's.
+template <typename T, bool ROT, int CLAMP>
+__global__ __launch_bounds__(512) void row_quant_spread_kernel(RowArgs a) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const bool real = row < a.M;
+  const int blk = tid >> 4, qr = lane & 3;
+  const int e0 = blk * 128 + ((lane >> 2) & 3) * 32 + qr * 8;
+  const bool ok = real && blk < a.nblk && e0 < a.K;
+  const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.ldx;
+  Raw<T> raw = load_raw32<T>(xrow, e0, ok);
+  // Chunks past the row (and padded rows) hold zeros: their codes are the
+  // zero-point's and they leave the row's min / max (which start at 0) alone.
+  uint32_t* w = reinterpret_cast<uint32_t*>(&raw);
+#pragma unroll
+  for (int k = 0; k < (int)(sizeof(Raw<T>) / 4); ++k) w[k] = ok ? w[k] : 0u;
+  float v[8];
+  if (ROT && sizeof(T) == 2) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bfly_f16x2(w[k], v[2 * k], v[2 * k + 1]);
+    fwht_chunk_tail(v);
+  } else {
+    to_f32(raw, v);
+    if (ROT) fwht_chunk(v);
+  }
+  float lsign = 1.0f;
+  if (ROT) {
+    fmac_dpp_xor1(v, (qr & 1) ? -1.0f : 1.0f);
+    fmac_dpp_xor2(v, (qr & 2) ? -1.0f : 1.0f);
+    bfly_swizzle<4>(v, (lane & 4) ? -1.0f : 1.0f);
+    bfly_swizzle<8>(v, (lane & 8) ? -1.0f : 1.0f);
+    lsign = (qr == 1 || qr == 2) ? -1.0f : 1.0f;  // these lanes hold -y
+  }
+  float mn = 0.0f, mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    mn = fminf(mn, v[i]);
+    mx = fmaxf(mx, v[i]);
+  }
+  if (lsign < 0.0f) {
+    const float t = mn;
+    mn = -mx;
+    mx = -t;
+  }
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  __shared__ float red[2][8];
+  if (lane == 0) {
+    red[0][wave] = mn;
+    red[1][wave] = mx;
+  }
+  __syncthreads();
+  mn = red[0][0];
+  mx = red[1][0];
+#pragma unroll
+  for (int k = 1; k < 8; ++k) {
+    mn = fminf(mn, red[0][k]);
+    mx = fmaxf(mx, red[1][k]);
+  }
+  const RowScale rs = row_scale<kAct>(mn, mx, a.clip, a.qmax);
+  RowScale rs_l = rs;
+  rs_l.y = lsign * rs.y;
+  uint32_t ev, od;
+  float dmax = 0.0f;
+  if (CLAMP)
+    act_chunk_fast(v, rs_l, ev, od, dmax);
+  else
+    act_chunk_fast_noclamp(v, rs_l, ev, od, dmax);
+  if (dmax >= rs.thr) act_chunk_exact(v, rs, lsign, ev, od);
+  // e0 < KP <= 4096 + 64: a block's 16 lanes store its 64 packed bytes.
+  if (blk < a.nblk && e0 < a.KP) {
+    if (a.packed)
+      *reinterpret_cast<uint32_t*>(a.packed + row * (a.KP / 2) + e0 / 2) = packed_nibbles(ev, od);
+    if (a.codes) store_codes<kAct>(a, row, e0, ev, od);
+  }
+  if (tid == 0) write_row_meta<kAct>(a, row, real, rs, 0);
+}
+
 // ------------------------------------------------------- small kernels
 
 // codes u8 [MP, KP] (0..15) -> packed [MP, KP/2]; kernel/w4a4.cu:65-68.
@@ -671,10 +765,26 @@ int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float 
   const int esize = dtype == DSCQ_F16 ? 2 : 4;
   a.vec = (K % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
           ((K * esize) % 16 == 0);
+  const bool rot = rotate_block != 0;
+  // Few activation rows of at most 32 blocks: the few-row kernel.
+  if (mode == kAct && a.vec && a.nblk <= 32 && MP <= kSpreadMaxRows) {
+    const bool noclamp = clip == 1.0f && qmax == 15.0f;
+#define DSCQ_SPREAD(T, R)                                                                    \
+  if (noclamp)                                                                               \
+    launch((row_quant_spread_kernel<T, R, 0>), dim3((unsigned)MP), dim3(512), stream, a);    \
+  else                                                                                       \
+    launch((row_quant_spread_kernel<T, R, 1>), dim3((unsigned)MP), dim3(512), stream, a);
+    if (dtype == DSCQ_F16) {
+      if (rot) { DSCQ_SPREAD(__half, true) } else { DSCQ_SPREAD(__half, false) }
+    } else {
+      if (rot) { DSCQ_SPREAD(float, true) } else { DSCQ_SPREAD(float, false) }
+    }
+#undef DSCQ_SPREAD
+    return launch_status("row_quant_spread_kernel");
+  }
   int wpr, iters;
   pick_shape(MP, a.nblk, &wpr, &iters);
   if (!a.vec) wpr = iters = 0;  // element-wise loads: streaming kernel only
-  const bool rot = rotate_block != 0;
 #define DSCQ_T(T)                                                                    \
   if (rot)                                                                           \
     return mode == kAct ? launch_rows_typed<T, true, kAct>(a, wpr, iters, stream)    \

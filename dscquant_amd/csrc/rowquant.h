@@ -320,6 +320,21 @@ __device__ __forceinline__ void fmac_dpp_xor2(float (&c)[8], float sgn) {
 }
 #undef DSCQ_FMAC_DPP8
 
+// Cross-lane butterfly through the LDS crossbar (ds_swizzle, no memory):
+// partner = lane ^ XOR within 32 lanes; the lane whose XOR bit is clear keeps
+// own + partner, the other partner - own -- fma(+-1, own, partner), rounded
+// exactly like the plain add / subtract.
+template <int XOR>
+__device__ __forceinline__ void bfly_swizzle(float (&c)[8], float sgn) {
+  constexpr int kPattern = 0x1F | (XOR << 10);  // bit mode: and 0x1f, xor XOR
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float p = __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, c[i]), kPattern));
+    c[i] = __builtin_fmaf(sgn, c[i], p);
+  }
+}
+
 // Index bits 3..6 of one block as c[4][8] in quad lane r; afterwards the lane
 // holds sign(r) * y with sign(r) = -1 for r = 1, 2 and +1 for r = 0, 3.
 __device__ __forceinline__ void fwht_block_tail_signed(float c[4][8], int r) {

@@ -68,6 +68,14 @@ QUANT_CASES = [
     # streaming kernel (K beyond the register capacity)
     (2, 40000, np.float16, 0, 1.0, True),
     (3, 40064, np.float16, 128, 1.0, True),
+    # few-row kernel (up to 512 padded rows of at most 32 blocks, a block over
+    # 16 lanes): the last row count it takes and the first it does not, a
+    # partial last block without rotation, the two-pass codes, fp32 with clamp
+    (512, 4096, np.float16, 128, 0.8, True),
+    (513, 4096, np.float16, 128, 1.0, True),
+    (300, 4000, np.float32, 0, 1.0, True),
+    (64, 2048, np.float16, 128, 1.0, False),
+    (2, 4096, np.float32, 128, 0.7, False),
 ]
 
 

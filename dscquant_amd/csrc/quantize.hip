@@ -22,7 +22,7 @@
 // wave's 16 blocks pass through LDS on the way out, so that each lane stores
 // 16 contiguous bytes.  Rows longer than the register capacity use the
 // two-pass streaming kernel at the end; up to 512 activation rows of at most
-// 32 blocks (decode and small batches) take the few-row kernel, a block over
+// 96 blocks (decode and small batches) take the few-row kernel, a block over
 // 16 lanes instead of 4.
 //
 // The per-element rules and the exactness argument of the fast division are
@@ -39,11 +39,15 @@ namespace dscq {
 namespace {
 
 constexpr int kThreads = 256;
-// Rows up to which activations of at most 32 blocks take the few-row kernel.
+// Rows up to which activations of at most 96 blocks take the few-row kernel.
 // Graph-replayed, K = 4096 with rotation, identical codes, register kernel /
 // few-row kernel: 1 row 2.63 / 2.28 us, 16 rows 3.05 / 2.50, 64 3.57 / 2.96,
 // 256 3.84 / 3.29, 512 4.30 / 4.08, 1024 5.77 / 5.80.
+// Up to three passes of 32 blocks (K <= 12288): 16 x 11008 4.17 -> 3.55 us,
+// 128 x 12288 4.78 -> 4.30, 512 x 11008 7.28 -> 6.87, 64 x 8192 3.72 -> 3.44;
+// 512 x 8192 equal (5.74 / 5.76).
 constexpr int64_t kSpreadMaxRows = 512;
+constexpr int kSpreadMaxPasses = 3;
 
 struct RowArgs {
   const void* x;       // [M, K] T
@@ -516,52 +520,65 @@ __global__ __launch_bounds__(kThreads) void row_quant_stream_kernel(RowArgs a) {
 }
 
 // ------------------------------------------------------- few-row kernel
-// Activation rows of at most 32 blocks (K <= 4096) when there are few of
-// them (decode): one row per 512-thread workgroup, a 128-element block over
-// 16 consecutive lanes, lane 4j + r holding elements j*32 + r*8 .. +7 (one
-// 16-byte load) -- 8 elements per lane instead of the register kernel's 32,
-// so each wave's chain of arithmetic is a quarter as long.  The transform
-// runs index bits 0-2 in the lane, bits 3-4 across the quad by DPP
-// (sign-folded as in the register kernel) and bits 5-6 across quads by
-// ds_swizzle xor 4 / xor 8, the same butterflies in the same order, so every
-// value, code, scale and zero-point is the register kernel's.
-template <typename T, bool ROT, int CLAMP>
+// Activation rows of at most 32 * PASSES blocks (K <= 4096 * PASSES) when
+// there are few of them (decode, small batches): one row per 512-thread
+// workgroup, a 128-element block over 16 consecutive lanes, lane 4j + r
+// holding elements j*32 + r*8 .. +7 (one 16-byte load) of blocks slot,
+// slot + 32, ... (slot = thread / 16) -- 8 elements per lane and pass instead
+// of the register kernel's 32 per block, so each wave's chain of arithmetic
+// is shorter.  The transform runs index bits 0-2 in the lane, bits 3-4 across
+// the quad by DPP (sign-folded as in the register kernel) and bits 5-6
+// across quads by ds_swizzle xor 4 / xor 8, the same butterflies in the same
+// order, so every value, code, scale and zero-point is the register kernel's.
+template <typename T, bool ROT, int CLAMP, int PASSES>
 __global__ __launch_bounds__(512) void row_quant_spread_kernel(RowArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
   const bool real = row < a.M;
-  const int blk = tid >> 4, qr = lane & 3;
-  const int e0 = blk * 128 + ((lane >> 2) & 3) * 32 + qr * 8;
-  const bool ok = real && blk < a.nblk && e0 < a.K;
+  const int qr = lane & 3;
   const T* xrow = static_cast<const T*>(a.x) + (real ? row : 0) * a.ldx;
-  Raw<T> raw = load_raw32<T>(xrow, e0, ok);
-  // Chunks past the row (and padded rows) hold zeros: their codes are the
-  // zero-point's and they leave the row's min / max (which start at 0) alone.
-  uint32_t* w = reinterpret_cast<uint32_t*>(&raw);
+  int e0[PASSES];
+  bool ok[PASSES];
+  Raw<T> raw[PASSES];
 #pragma unroll
-  for (int k = 0; k < (int)(sizeof(Raw<T>) / 4); ++k) w[k] = ok ? w[k] : 0u;
-  float v[8];
-  if (ROT && sizeof(T) == 2) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) bfly_f16x2(w[k], v[2 * k], v[2 * k + 1]);
-    fwht_chunk_tail(v);
-  } else {
-    to_f32(raw, v);
-    if (ROT) fwht_chunk(v);
+  for (int c = 0; c < PASSES; ++c) {
+    const int blk = c * 32 + (tid >> 4);
+    e0[c] = blk * 128 + ((lane >> 2) & 3) * 32 + qr * 8;
+    ok[c] = real && blk < a.nblk && e0[c] < a.K;
+    raw[c] = load_raw32<T>(xrow, e0[c], ok[c]);
   }
-  float lsign = 1.0f;
-  if (ROT) {
-    fmac_dpp_xor1(v, (qr & 1) ? -1.0f : 1.0f);
-    fmac_dpp_xor2(v, (qr & 2) ? -1.0f : 1.0f);
-    bfly_swizzle<4>(v, (lane & 4) ? -1.0f : 1.0f);
-    bfly_swizzle<8>(v, (lane & 8) ? -1.0f : 1.0f);
-    lsign = (qr == 1 || qr == 2) ? -1.0f : 1.0f;  // these lanes hold -y
-  }
+  const float s1 = (qr & 1) ? -1.0f : 1.0f, s2 = (qr & 2) ? -1.0f : 1.0f;
+  const float s4 = (lane & 4) ? -1.0f : 1.0f, s8 = (lane & 8) ? -1.0f : 1.0f;
+  // Lanes r = 1, 2 hold -y after the DPP stages.
+  const float lsign = (ROT && (qr == 1 || qr == 2)) ? -1.0f : 1.0f;
+  float v[PASSES][8];
   float mn = 0.0f, mx = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    mn = fminf(mn, v[i]);
-    mx = fmaxf(mx, v[i]);
+  for (int c = 0; c < PASSES; ++c) {
+    // Chunks past the row (and padded rows) hold zeros: their codes are the
+    // zero-point's and they leave the row's min / max (which start at 0) alone.
+    uint32_t* w = reinterpret_cast<uint32_t*>(&raw[c]);
+#pragma unroll
+    for (int k = 0; k < (int)(sizeof(Raw<T>) / 4); ++k) w[k] = ok[c] ? w[k] : 0u;
+    if (ROT && sizeof(T) == 2) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) bfly_f16x2(w[k], v[c][2 * k], v[c][2 * k + 1]);
+      fwht_chunk_tail(v[c]);
+    } else {
+      to_f32(raw[c], v[c]);
+      if (ROT) fwht_chunk(v[c]);
+    }
+    if (ROT) {
+      fmac_dpp_xor1(v[c], s1);
+      fmac_dpp_xor2(v[c], s2);
+      bfly_swizzle<4>(v[c], s4);
+      bfly_swizzle<8>(v[c], s8);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      mn = fminf(mn, v[c][i]);
+      mx = fmaxf(mx, v[c][i]);
+    }
   }
   if (lsign < 0.0f) {
     const float t = mn;
@@ -586,18 +603,28 @@ __global__ __launch_bounds__(512) void row_quant_spread_kernel(RowArgs a) {
   const RowScale rs = row_scale<kAct>(mn, mx, a.clip, a.qmax);
   RowScale rs_l = rs;
   rs_l.y = lsign * rs.y;
-  uint32_t ev, od;
-  float dmax = 0.0f;
-  if (CLAMP)
-    act_chunk_fast(v, rs_l, ev, od, dmax);
-  else
-    act_chunk_fast_noclamp(v, rs_l, ev, od, dmax);
-  if (dmax >= rs.thr) act_chunk_exact(v, rs, lsign, ev, od);
-  // e0 < KP <= 4096 + 64: a block's 16 lanes store its 64 packed bytes.
-  if (blk < a.nblk && e0 < a.KP) {
-    if (a.packed)
-      *reinterpret_cast<uint32_t*>(a.packed + row * (a.KP / 2) + e0 / 2) = packed_nibbles(ev, od);
-    if (a.codes) store_codes<kAct>(a, row, e0, ev, od);
+#pragma unroll
+  for (int c = 0; c < PASSES; ++c) {
+    uint32_t ev, od;
+    float dmax = 0.0f;
+    if (CLAMP)
+      act_chunk_fast(v[c], rs_l, ev, od, dmax);
+    else
+      act_chunk_fast_noclamp(v[c], rs_l, ev, od, dmax);
+    if (dmax >= rs.thr) {
+      // Keeps the IEEE divisions behind the branch (near-ties are rare); the
+      // compiler would otherwise compute them for every chunk and select.
+      asm volatile("" ::: "memory");
+      act_chunk_exact(v[c], rs, lsign, ev, od);
+    }
+    // A block's 16 lanes store its 64 packed bytes; chunks in [K, KP) hold
+    // the zero-point's code.
+    if (c * 32 + (tid >> 4) < a.nblk && e0[c] < a.KP) {
+      if (a.packed)
+        *reinterpret_cast<uint32_t*>(a.packed + row * (a.KP / 2) + e0[c] / 2) =
+            packed_nibbles(ev, od);
+      if (a.codes) store_codes<kAct>(a, row, e0[c], ev, od);
+    }
   }
   if (tid == 0) write_row_meta<kAct>(a, row, real, rs, 0);
 }
@@ -766,20 +793,30 @@ int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float 
   a.vec = (K % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0) &&
           ((K * esize) % 16 == 0);
   const bool rot = rotate_block != 0;
-  // Few activation rows of at most 32 blocks: the few-row kernel.
-  if (mode == kAct && a.vec && a.nblk <= 32 && MP <= kSpreadMaxRows) {
+  // Few activation rows of at most 32 * kSpreadMaxPasses blocks: the few-row kernel.
+  if (mode == kAct && a.vec && a.nblk <= 32 * kSpreadMaxPasses && MP <= kSpreadMaxRows) {
     const bool noclamp = clip == 1.0f && qmax == 15.0f;
-#define DSCQ_SPREAD(T, R)                                                                    \
-  if (noclamp)                                                                               \
-    launch((row_quant_spread_kernel<T, R, 0>), dim3((unsigned)MP), dim3(512), stream, a);    \
-  else                                                                                       \
-    launch((row_quant_spread_kernel<T, R, 1>), dim3((unsigned)MP), dim3(512), stream, a);
+    const int passes = (a.nblk + 31) / 32;
+#define DSCQ_SPREAD_P(T, R, C)                                                                  \
+  if (passes == 1)                                                                              \
+    launch((row_quant_spread_kernel<T, R, C, 1>), dim3((unsigned)MP), dim3(512), stream, a);    \
+  else if (passes == 2)                                                                         \
+    launch((row_quant_spread_kernel<T, R, C, 2>), dim3((unsigned)MP), dim3(512), stream, a);    \
+  else                                                                                          \
+    launch((row_quant_spread_kernel<T, R, C, 3>), dim3((unsigned)MP), dim3(512), stream, a);
+#define DSCQ_SPREAD(T, R)  \
+  if (noclamp) {           \
+    DSCQ_SPREAD_P(T, R, 0) \
+  } else {                 \
+    DSCQ_SPREAD_P(T, R, 1) \
+  }
     if (dtype == DSCQ_F16) {
       if (rot) { DSCQ_SPREAD(__half, true) } else { DSCQ_SPREAD(__half, false) }
     } else {
       if (rot) { DSCQ_SPREAD(float, true) } else { DSCQ_SPREAD(float, false) }
     }
 #undef DSCQ_SPREAD
+#undef DSCQ_SPREAD_P
     return launch_status("row_quant_spread_kernel");
   }
   int wpr, iters;

@@ -76,6 +76,11 @@ QUANT_CASES = [
     (300, 4000, np.float32, 0, 1.0, True),
     (64, 2048, np.float16, 128, 1.0, False),
     (2, 4096, np.float32, 128, 0.7, False),
+    # ... with two and three passes of 32 blocks (K up to 12288)
+    (16, 11008, np.float16, 128, 1.0, True),
+    (64, 8192, np.float16, 128, 0.9, True),
+    (2, 12288, np.float32, 128, 1.0, False),
+    (100, 9000, np.float32, 0, 1.0, True),
 ]
 
 

@@ -870,25 +870,32 @@ int launch_cfg(GemmArgs g, hipStream_t stream) {
 // Partial 16 x 16 sums meet in LDS; the epilogue is the reference's.
 // Bytes per launch: N * KP / 2 (weights) + the small A, read once per column
 // block from L2.
+// Where the grid would take two or more rounds over the CUs, a workgroup
+// owns two or three tiles of 16 columns and loads its A pieces once for them.
 // GATED (dscq_matmul_silu_mul at M <= 16): output column n of h [M, N / 2]
 // takes weight row 128 (n / 64) + n % 64 (gate) and that row + 64 (up); both
 // are streamed by the same workgroup and combined in the epilogue with the
 // gated epilogue's silu_mul_f16x2.
-template <typename OutT, bool BIAS, bool GATED = false>
+// NT > 1 (not gated): the workgroup owns NT tiles of 16 columns, n0 + 16 t,
+// each wave's A pieces loaded once and used for all of them.
+template <typename OutT, bool BIAS, bool GATED = false, int NT = 1>
 __global__ __launch_bounds__(512) void w4a4_gemv_kernel(GemmArgs g) {
   constexpr int WAVES = 8;
-  constexpr int NB = GATED ? 2 : 1;  // weight row streams (gate, up)
+  static_assert(!GATED || NT == 1, "the gated form owns one tile");
+  constexpr int NB = GATED ? 2 : NT;  // weight row streams (gate, up / the tiles)
   __shared__ int32_t part[NB][WAVES][16][16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t n0 = (int64_t)blockIdx.x * 16, m0 = (int64_t)blockIdx.y * 16;
+  const int64_t n0 = (int64_t)blockIdx.x * 16 * NT, m0 = (int64_t)blockIdx.y * 16;
   const int r = lane & 15, grp = lane >> 4;
   const int64_t KB = g.KP / 2;
   const int64_t nblk = (KB + 63) / 64;
   const int64_t per = (nblk + WAVES - 1) / WAVES;
   const int64_t b0 = wave * per, b1 = min(b0 + per, nblk);
   const int64_t NOUT = GATED ? g.N / 2 : g.N;  // output columns
+  // Weight row of stream s for output column n of tile 0 (gated: gate / up
+  // row; else the row of tile s, 16 s columns on).
   auto wrow = [&](int64_t n, int s) -> int64_t {
-    return GATED ? 128 * (n / 64) + n % 64 + 64 * s : n;
+    return GATED ? 128 * (n / 64) + n % 64 + 64 * s : n + 16 * s;
   };
   const uint8_t* arow = g.a + min(m0 + r, g.arows - 1) * KB;
   const uint8_t* brow[NB];
@@ -907,10 +914,12 @@ __global__ __launch_bounds__(512) void w4a4_gemv_kernel(GemmArgs g) {
   int32_t e_sum[NB];
 #pragma unroll
   for (int s = 0; s < NB; ++s) {
-    const int64_t nc = min(GATED ? wrow(nout, s) : n0 + nl, g.brows - 1);
+    const int64_t nc = min(GATED ? wrow(nout, s) : n0 + 16 * s + nl, g.brows - 1);
     e_sw[s] = g.sw[nc];
     e_sum[s] = g.sums[nc];
-    e_b[s] = BIAS ? (float)static_cast<const OutT*>(g.bias)[min(wrow(nout, s), g.N - 1)] : 0.0f;
+    e_b[s] = BIAS ? (float)static_cast<const OutT*>(
+                        g.bias)[min(GATED ? wrow(nout, s) : n0 + 16 * s + nl, g.N - 1)]
+                  : 0.0f;
   }
 
   v4i acc[NB];
@@ -983,26 +992,53 @@ __global__ __launch_bounds__(512) void w4a4_gemv_kernel(GemmArgs g) {
     if (BIAS) res[s] = res[s] + e_b[s];
   }
   const int64_t m = m0 + ml, n = n0 + nl;
-  if (m >= g.M || n >= NOUT) return;
+  if (m >= g.M) return;
   if constexpr (GATED) {
+    if (n >= NOUT) return;
     const uint32_t gb = __half_as_ushort(to_out<__half>(res[0]));
     const uint32_t ub = __half_as_ushort(to_out<__half>(res[1]));
     static_cast<uint16_t*>(g.out)[m * NOUT + n] = (uint16_t)(silu_mul_f16x2(gb, ub) & 0xFFFFu);
   } else {
-    static_cast<OutT*>(g.out)[m * g.N + n] = to_out<OutT>(res[0]);
-    if (g.raw) g.raw[m * g.N + n] = raw[0];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int64_t nt = n + 16 * t;
+      if (nt >= g.N) break;
+      static_cast<OutT*>(g.out)[m * g.N + nt] = to_out<OutT>(res[t]);
+      if (g.raw) g.raw[m * g.N + nt] = raw[t];
+    }
   }
 }
 
 template <typename OutT, bool GATED = false>
 int launch_gemv(GemmArgs g, hipStream_t stream) {
-  const int64_t gx = ((GATED ? g.N / 2 : g.N) + 15) / 16, gy = (g.M + 15) / 16;
+  const int64_t tiles = ((GATED ? g.N / 2 : g.N) + 15) / 16, gy = (g.M + 15) / 16;
+  // Tiles per workgroup as in the fused decode kernel: up to three tiles per
+  // CU in one round, two beyond.  Quantize + this kernel, graph-replayed,
+  // weights from HBM, one tile / NT: M = 8, N = 11008 11.07 / 10.81 us (two
+  // tiles: 12.25); M = 16, N = 11008 12.56 / 11.25; M = 16, N = 14336 14.93 /
+  // 13.37; M = 8, N = 28672 19.3 / 18.8; M = 32, N = 4096 9.92 / 9.21.
+  const int64_t cus = cu_count(), per_cu = (tiles * gy + cus - 1) / cus;
+  const int nt = GATED ? 1 : per_cu > 3 ? 2 : (int)std::max<int64_t>(1, per_cu);
+  const int64_t gx = (tiles + nt - 1) / nt;
   if (gx > 0x7FFFFFFF || gy > 65535) return fail("matmul: grid too large");
   const dim3 grid((unsigned)gx, (unsigned)gy), block(512);
-  if (g.bias)
-    launch((w4a4_gemv_kernel<OutT, true, GATED>), grid, block, stream, g);
-  else
-    launch((w4a4_gemv_kernel<OutT, false, GATED>), grid, block, stream, g);
+#define DSCQ_GEMV(NTV)                                                            \
+  if (g.bias)                                                                     \
+    launch((w4a4_gemv_kernel<OutT, true, GATED, NTV>), grid, block, stream, g);   \
+  else                                                                            \
+    launch((w4a4_gemv_kernel<OutT, false, GATED, NTV>), grid, block, stream, g);
+  if constexpr (GATED) {
+    DSCQ_GEMV(1)
+  } else {
+    if (nt == 1) {
+      DSCQ_GEMV(1)
+    } else if (nt == 2) {
+      DSCQ_GEMV(2)
+    } else {
+      DSCQ_GEMV(3)
+    }
+  }
+#undef DSCQ_GEMV
   return launch_status("w4a4_gemv_kernel");
 }
 

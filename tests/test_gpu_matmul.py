@@ -97,6 +97,12 @@ MM_CASES = [
     (3584, 4096, 4352, False, True, False),
     (2048, 8192, 4160, True, True, False),
     (2048, 8192, 256, False, False, False),
+    # skinny-M workgroups with two or three tiles of 16 columns: N = 14336
+    # (two), ragged N = 8200 (three, the last workgroup short), forced decode
+    # over three row blocks with ragged N (two)
+    (16, 14336, 4096, True, True, False),
+    (8, 8200, 4096, True, False, False),
+    (40, 5000, 1024, False, False, True),
 ]
 
 

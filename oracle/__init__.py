@@ -1,6 +1,6 @@
 """CPU oracle for the DSCQuant W4A4 linear-layer path.
 
-TEST INFRASTRUCTURE ONLY.  This package is the checker the HIP product path
+TEST INFRASTRUCTURE ONLY.  This package is the reference the HIP product path
 (``dscquant_amd``) is compared against.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
 it; the product never does, and never falls back to it.

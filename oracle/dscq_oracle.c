@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the DSCQuant W4A4 linear-layer path.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker the HIP kernels are
+ * TEST INFRASTRUCTURE ONLY.  This file is the reference the HIP kernels are
  * compared against; nothing in the product (dscquant_amd/) links, loads or
  * calls it.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
  * leg may use it.

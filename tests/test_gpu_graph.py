@@ -3,8 +3,10 @@ times it: every replay must read the current contents of its input buffers and
 give, bit for bit, what eager calls give on the same data.  Each replay is
 followed by eager work on the same stream and a synchronisation, and the inputs
 change between replays.  Covered: rotate+quantize+pack -> pipelined GEMM
-(prefill shape class), quantize -> skinny-M GEMM (16 tokens), the fused decode
-kernel, and the SiLU-gated requantization.
+(prefill shape class, the prefill shape itself), quantize -> skinny-M GEMM (16
+tokens, one and three column tiles per workgroup), the fused decode kernel (one
+and three tiles per workgroup, both product forms), and the SiLU-gated
+requantization.
 """
 import numpy as np
 import pytest
@@ -43,7 +45,8 @@ def _replay_and_compare(fn, inputs):
             assert torch.equal(o, r), f"replay {rep} differs from eager"
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 4096, 1024), (16, 4096, 4096), (128, 11008, 4096)])
+@pytest.mark.parametrize("M,K,N", [(256, 4096, 1024), (16, 4096, 4096), (128, 11008, 4096),
+                                   (16, 4096, 11008), (2048, 4096, 4096)])
 def test_quantize_matmul_graph(gpu, M, K, N):
     print(f"graph quantize+matmul M{M} K{K} N{N}", flush=True)
     pw, sw, sums = w4a4.pack_weight(torch.from_numpy(weights(N, K, seed=9)).to(gpu), 1.0, 128)
@@ -59,8 +62,9 @@ def test_quantize_matmul_graph(gpu, M, K, N):
     _replay_and_compare(run, xs)
 
 
-def test_linear_decode_graph(gpu):
-    M, K, N = 2, 4096, 4096
+@pytest.mark.parametrize("M,N", [(2, 4096), (4, 11008), (1, 11008)])
+def test_linear_decode_graph(gpu, M, N):
+    K = 4096
     print(f"graph linear_decode M{M} K{K} N{N}", flush=True)
     assert w4a4.linear_decode_supported(M, K)
     pw, sw, sums = w4a4.pack_weight(torch.from_numpy(weights(N, K, seed=5)).to(gpu), 1.0, 128)

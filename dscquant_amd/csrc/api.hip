@@ -2,6 +2,7 @@
 // checks with the reference extension's messages (kernel/w4a4.cu:164-225),
 // then asynchronous launches on the caller's stream.
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -52,17 +53,18 @@ KernelEvents take_kernel_events() {
 void arm_kernel_events(KernelEvents ev) { g_kernel_events = ev; }
 
 int cu_count() {
-  static int cached[64] = {};
+  // Per device, filled on first use; concurrent first calls store the same value.
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 int fail(const char* fmt, ...) {

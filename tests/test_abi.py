@@ -324,3 +324,33 @@ def test_interleave_gate_up_order():
     assert torch.equal(w4a4.interleave_gate_up(g2, u2)[:, 0], il)
     with pytest.raises(RuntimeError):
         w4a4.interleave_gate_up(gate[:100], up[:100])
+
+
+def test_last_error_is_per_thread():
+    """dscq_last_error() reports the calling thread's own last failure: two
+    threads failing with different messages, interleaved, each read theirs."""
+    import threading
+    L = _lib.lib()
+    dummy = 16
+    barrier = threading.Barrier(2, timeout=10)
+    seen = {}
+
+    def worker(name, dtype, M, want):
+        msgs = []
+        for _ in range(200):
+            rc = L.dscq_quantize(dummy, dtype, M, 64, 1.0, 1, 0, dummy, dummy, dummy, None, None)
+            assert rc == -1
+            barrier.wait()
+            msgs.append(L.dscq_last_error().decode())
+            barrier.wait()
+        seen[name] = set(msgs)
+        assert seen[name] == {want}
+
+    ts = [threading.Thread(target=worker, args=("a", 7, 4, "Only FP16 and FP32 inputs are supported")),
+          threading.Thread(target=worker, args=("b", 0, 0, "Require 1<=M<=65535 and 1<=K<=1048576"))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert seen == {"a": {"Only FP16 and FP32 inputs are supported"},
+                    "b": {"Require 1<=M<=65535 and 1<=K<=1048576"}}

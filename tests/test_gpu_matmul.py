@@ -193,3 +193,21 @@ def test_end_to_end_config_data(gpu, M, N, K, rot):
     np.testing.assert_array_equal(raw.cpu().numpy(), raw_ref)
     out_ref = native.restore(raw_ref, sx_ref, zx_ref, sw_ref, sums_ref, None)
     np.testing.assert_array_equal(out.cpu().numpy(), out_ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8, 1048576), (65535, 8, 64), (3, 24, 262144)])
+def test_matmul_size_limits(gpu, M, N, K):
+    """The largest K (2^20, the quantize limit) and M (65535) the path accepts,
+    random nibbles, raw accumulators against the oracle's integer GEMM."""
+    print(f"matmul limits M{M} N{N} K{K}", flush=True)
+    a, b, sx, zx, sw, sums = _operands(M, N, K, seed=M + N + K)
+    T = lambda v: torch.from_numpy(v).to(gpu)  # noqa: E731
+    out, raw = w4a4.matmul(T(a), T(b), T(sx), T(zx), T(sw), T(sums),
+                           torch.empty(0, dtype=torch.float32, device=gpu), M, N,
+                           fused=False, fp32=True)
+    torch.cuda.synchronize()
+    raw_ref = native.gemm_raw(a, b, M, N)
+    np.testing.assert_array_equal(raw.cpu().numpy(), raw_ref)
+    np.testing.assert_array_equal(out.cpu().numpy(),
+                                  native.restore(raw_ref, sx, zx, sw, sums, None,
+                                                 out_dtype=np.float32))

@@ -76,6 +76,11 @@ QUANT_CASES = [
     (300, 4000, np.float32, 0, 1.0, True),
     (64, 2048, np.float16, 128, 1.0, False),
     (2, 4096, np.float32, 128, 0.7, False),
+    # the limits: K = 2^20 (streaming kernel, with and without rotation) and
+    # M = 65535 (65536 padded rows)
+    (2, 1048576, np.float16, 128, 1.0, True),
+    (1, 1048576, np.float32, 0, 0.8, True),
+    (65535, 64, np.float16, 0, 1.0, True),
     # ... with two and three passes of 32 blocks (K up to 12288)
     (16, 11008, np.float16, 128, 1.0, True),
     (64, 8192, np.float16, 128, 0.9, True),

@@ -70,7 +70,8 @@ struct DecodeArgs {
 // 8 or 12 >= the blocks a wave owns); DOT form: 16-byte pieces of the lane's
 // weight row (4, 8 or 12 >= ceil(KB / 512)) -- a compile-time count so the
 // loads are unconditional: a load behind a branch makes the wait for an
-// earlier load conservative.
+// earlier load conservative.  NT: tiles of 16 output columns per workgroup
+// (1-3; the v_dot8 form only with PER = 4), each with its own weight pieces.
 //
 // Activation layouts (both run the quantize kernel's butterflies in the same
 // order, so every value is rounded identically; rowquant.h):

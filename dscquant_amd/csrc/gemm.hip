@@ -325,8 +325,24 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     s0 = p * g.kslices;
     part = g.part + (int64_t)p * g.M * g.N;
   }
-  const int tile_m = bid / g.tiles_n;
-  const int tile_n = bid % g.tiles_n;
+  int tile_m = bid / g.tiles_n;
+  int tile_n = bid % g.tiles_n;
+  if constexpr (!SPLIT && BM == 256) {
+    // Whole rounds of 256 x 128 tiles with wide N (>= 128 column tiles):
+    // workgroup b runs on XCD b % 8, so each XCD's 32 workgroups of a round
+    // take a 4 x 8 block of tiles (A read once per round, 2048 B rows instead
+    // of up to all of B per XCD).  Measured, row-major order / blocks:
+    // 4096 x 28672 x 8192 722 / 708 us, 2048 x 16384 x 4096 112.5 / 111.7 us;
+    // at N = 8192 no gain (206.2 / 207.2 us), so narrower N keeps row order.
+    const int tiles_m = (int)((g.M + BM - 1) / BM);
+    if (g.tiles_n >= 128 && g.tiles_n % 8 == 0 && tiles_m % 4 == 0 &&
+        (tiles_m * g.tiles_n) % 256 == 0) {
+      const int grp = (bid >> 8) * 8 + (bid & 7), l = (bid & 255) >> 3;
+      const int gm = tiles_m / 4;
+      tile_m = (grp % gm) * 4 + (l & 3);
+      tile_n = (grp / gm) * 8 + (l >> 2);
+    }
+  }
   const int64_t m0 = (int64_t)tile_m * BM;
   const int64_t n0 = (int64_t)tile_n * BN;
   const int64_t KB = g.KP / 2;

@@ -97,6 +97,9 @@ MM_CASES = [
     (3584, 4096, 4352, False, True, False),
     (2048, 8192, 4160, True, True, False),
     (2048, 8192, 256, False, False, False),
+    # wide N in whole rounds: each XCD's workgroups of a round on a 4 x 8 block
+    # of tiles (1024 x 16384: two rounds of 256 tiles)
+    (1024, 16384, 320, True, False, False),
     # skinny-M workgroups with two or three tiles of 16 columns: N = 14336
     # (two), ragged N = 8200 (three, the last workgroup short), forced decode
     # over three row blocks with ragged N (two)

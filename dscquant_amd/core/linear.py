@@ -23,10 +23,15 @@ Derived state is cached on the module, never in its state_dict:
 * the clip values as Python floats, so a steady-state forward issues no
   device-to-host read and can be captured in a HIP graph.
 
-A change is seen through tensor identity and PyTorch's version counter:
-in-place updates under ``torch.no_grad()``, ``load_state_dict``, optimizer
-steps and assigning new tensors all bump it.  Writes through ``.data`` do
-not; call ``invalidate_cache()`` after such a write.
+A change is seen through tensor identity, PyTorch's version counter, the
+storage address, dtype and device: in-place updates under ``torch.no_grad()``,
+``load_state_dict``, optimizer steps, assigning new tensors and the module
+casts and moves (``.half()``, ``.to()``, ``.cuda()``) are all seen.  In-place
+writes through ``.data`` are not; call ``invalidate_cache()`` after such a
+write.
+
+An empty batch (``x`` with no rows) returns an empty ``[..., 0, N]`` output in
+``x``'s dtype without launching anything, as ``F.linear`` does.
 
 Other bit widths run the reference composition with GPU-computed codes.
 ``rotate_block`` (default 0) is an attribute like ``enabled``: set it to 128
@@ -51,13 +56,17 @@ _SCALARS = (int, float, bool, str, type(None))
 def _stamp(objects):
     """(key, pins) for a sequence of (name, value) pairs.
 
-    The key holds ids and version counters only (plain ints, safe to compare
-    with ==); ``pins`` keeps the tensors alive so that their ids cannot be
-    reused by new tensors while the key is held."""
+    A tensor is keyed by identity, version counter, storage address, dtype and
+    device (plain values, safe to compare with ==): ``Module.half()`` / ``.to()``
+    / ``.cuda()`` swap a parameter's ``.data`` without changing its identity or
+    version, but never its storage, dtype and device together.  ``pins`` keeps
+    the tensors alive so that their ids cannot be reused by new tensors while
+    the key is held."""
     key, pins = [], []
     for name, value in objects:
         if isinstance(value, torch.Tensor):
-            key.append((name, id(value), value._version))
+            key.append((name, id(value), value._version, value.data_ptr(), value.dtype,
+                        value.device))
             pins.append(value)
         elif isinstance(value, _SCALARS):
             key.append((name, type(value).__name__, value))
@@ -148,18 +157,19 @@ class QuantLinear(nn.Module):
         self._fold = None     # (key, pins, weight, bias)
         self._pack = None     # (key, pins, (packed, sw, sums))
         self._biases = {}     # dtype -> (key, pins, bias in that dtype)
-        self._clips = {}      # name -> (parameter, version, float)
+        self._clips = {}      # name -> (parameter, stamp, float)
         self._fold_gen = getattr(self, "_fold_gen", 0) + 1
 
     def clip_value(self, name: str) -> float:
         """``weight_clip`` / ``activation_clip`` as a float, read from the device
         only when the parameter changed."""
         p = getattr(self, name)
+        stamp = (p._version, p.data_ptr(), p.dtype, p.device)
         hit = self._clips.get(name)
-        if hit is not None and hit[0] is p and hit[1] == p._version:
+        if hit is not None and hit[0] is p and hit[1] == stamp:
             return hit[2]
         value = float(p.detach().float().item())
-        self._clips[name] = (p, p._version, value)
+        self._clips[name] = (p, stamp, value)
         return value
 
     def _fold_key(self, interface):
@@ -234,10 +244,19 @@ class QuantLinear(nn.Module):
     def _forward_w4a4(self, x):
         if x.requires_grad and torch.is_grad_enabled():
             raise RuntimeError("the W4A4 HIP path is inference-only (codes carry no gradient)")
-        packed_w, sw, sums = self.packed_weight()
-        N = self.base.weight.shape[0]
+        N, KW = self.base.weight.shape
         K = x.shape[-1]
         lead = x.shape[:-1]
+        if K != KW:
+            # F.linear's own check (core/linear.py:52); packing pads K to 64, so the
+            # kernels alone would not see a mismatch inside one padding step.
+            raise RuntimeError(f"mat1 and mat2 shapes cannot be multiplied "
+                               f"({x.numel() // max(K, 1)}x{K} and {KW}x{N})")
+        if x.numel() == 0:
+            # An empty batch: F.linear returns [..., 0, N] in x's dtype
+            # (core/linear.py:48-52); nothing is launched.
+            return torch.empty((*lead, N), dtype=x.dtype, device=x.device)
+        packed_w, sw, sums = self.packed_weight()
         xr = x.reshape(-1, K)
         if xr.dtype not in (torch.float16, torch.float32):
             xr = xr.float()

@@ -125,6 +125,7 @@ int dscq_device_supported(void) {
 int dscq_quantize(const void* x, int x_dtype, int64_t M, int64_t K, float clip, int fused,
                   int rotate_block, uint8_t* packed, float* scales, int32_t* zeros,
                   uint8_t* codes, void* stream) {
+  DisarmOnExit disarm;
   // kernel/w4a4.cu:165-168
   if (!valid_dtype(x_dtype)) return fail("Only FP16 and FP32 inputs are supported");
   if (!(M > 0 && M <= 65535 && K > 0 && K <= 1048576))
@@ -152,6 +153,7 @@ int dscq_linear_decode(const void* x, int x_dtype, int64_t M, int64_t K, float c
                        int rotate_block, const uint8_t* b, const float* sw,
                        const int32_t* sums, const void* bias, int64_t N, int out_fp32,
                        void* out, void* stream) {
+  DisarmOnExit disarm;
   if (!valid_dtype(x_dtype)) return fail("Only FP16 and FP32 inputs are supported");
   if (!linear_decode_fits(M, K))
     return fail("linear_decode: M=%lld, K=%lld exceed the fused decode kernel (quantize + "
@@ -171,6 +173,7 @@ int dscq_linear_decode_supported(int64_t M, int64_t K) { return linear_decode_fi
 int dscq_silu_mul_quantize(const void* gate, const void* up, int64_t ld, int64_t M,
                            int64_t N, float clip, int rotate_block, uint8_t* packed,
                            float* scales, int32_t* zeros, void* h, void* stream) {
+  DisarmOnExit disarm;
   if (!(M > 0 && M <= 65535 && N > 0 && N <= 32768))
     return fail("silu_mul_quantize: require 1<=M<=65535 and 1<=N<=32768");
   if (ld < N) return fail("silu_mul_quantize: row stride %lld is below N=%lld", (long long)ld,
@@ -186,6 +189,7 @@ int dscq_matmul_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
                          const int32_t* zx, const float* sw, const int32_t* sums,
                          const void* bias, int64_t M, int64_t N, int64_t KP, void* h,
                          void* stream) {
+  DisarmOnExit disarm;
   if (!(M > 0 && M <= 65535)) return fail("matmul_silu_mul: require 1<=M<=65535");
   if (!a || !b_gu || !sx || !zx || !sw || !sums || !h) return fail("matmul_silu_mul: null buffer");
   if (!gemm_silu_mul_fits(M, N, KP, h))
@@ -199,6 +203,7 @@ int dscq_matmul_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
 int dscq_activation_codes(const void* x, int x_dtype, int64_t M, int64_t K, float clip,
                           int bits, int rotate_block, uint8_t* codes, float* scales,
                           int32_t* zeros, void* stream) {
+  DisarmOnExit disarm;
   if (!valid_dtype(x_dtype)) return fail("Only FP16 and FP32 inputs are supported");
   if (!(M > 0 && M <= 65535 && K > 0 && K <= 1048576))
     return fail("Require 1<=M<=65535 and 1<=K<=1048576");
@@ -214,6 +219,7 @@ int dscq_activation_codes(const void* x, int x_dtype, int64_t M, int64_t K, floa
 int dscq_pack_weight(const void* w, int w_dtype, int64_t N, int64_t K, float clip,
                      int rotate_block, uint8_t* packed, float* sw, int32_t* sums,
                      int8_t* codes, void* stream) {
+  DisarmOnExit disarm;
   if (!valid_dtype(w_dtype)) return fail("Only FP16 and FP32 inputs are supported");
   if (!(N > 0 && N <= 1048576 && K > 0 && K <= 1048576))
     return fail("Require 1<=N<=1048576 and 1<=K<=1048576");
@@ -228,6 +234,7 @@ int dscq_pack_weight(const void* w, int w_dtype, int64_t N, int64_t K, float cli
 int dscq_weight_codes(const void* w, int w_dtype, int64_t N, int64_t K, float clip,
                       int bits, int rotate_block, int8_t* codes, float* scales,
                       void* stream) {
+  DisarmOnExit disarm;
   if (!valid_dtype(w_dtype)) return fail("Only FP16 and FP32 inputs are supported");
   if (!(N > 0 && N <= 1048576 && K > 0 && K <= 1048576))
     return fail("Require 1<=N<=1048576 and 1<=K<=1048576");
@@ -245,6 +252,7 @@ int dscq_matmul(const uint8_t* a, const uint8_t* b, const float* sx, const int32
                 const float* sw, const int32_t* sums, const void* bias, int64_t M,
                 int64_t N, int64_t KP, int fused, int force_decode, int out_fp32,
                 void* out, int32_t* raw, void* stream) {
+  DisarmOnExit disarm;
   // kernel/w4a4.cu:197
   if (!(M > 0 && M <= 65535 && N > 0 && KP > 0 && KP <= 1048576 && KP % 64 == 0))
     return fail("Invalid dimensions");
@@ -269,6 +277,7 @@ int dscq_matmul_ws(const uint8_t* a, const uint8_t* b, const float* sx, const in
                    int64_t N, int64_t KP, int fused, int force_decode, int out_fp32,
                    void* out, int32_t* raw, void* workspace, int64_t workspace_bytes,
                    void* stream) {
+  DisarmOnExit disarm;
   if (!(M > 0 && M <= 65535 && N > 0 && KP > 0 && KP <= 1048576 && KP % 64 == 0))
     return fail("Invalid dimensions");
   if (N > 0x7FFFFFFFLL) return fail("Invalid dimensions");
@@ -283,6 +292,7 @@ int dscq_matmul_ws(const uint8_t* a, const uint8_t* b, const float* sx, const in
 
 int dscq_pack_int4(const int8_t* codes, int64_t R, int64_t C, uint8_t* packed,
                    void* stream) {
+  DisarmOnExit disarm;
   if (R < 0 || C < 0) return fail("pack_int4: negative shape");
   if ((R && C) && (!codes || !packed)) return fail("pack_int4: null buffer");
   return pack_int4(codes, R, C, packed, static_cast<hipStream_t>(stream));
@@ -290,6 +300,7 @@ int dscq_pack_int4(const int8_t* codes, int64_t R, int64_t C, uint8_t* packed,
 
 int dscq_unpack_int4(const uint8_t* packed, int64_t R, int64_t CB, int64_t width,
                      int8_t* codes, void* stream) {
+  DisarmOnExit disarm;
   if (R < 0 || CB < 0 || width < 0 || width > 2 * CB)
     return fail("unpack_int4: width must be in [0, 2 * packed columns]");
   if ((R && width) && (!codes || !packed)) return fail("unpack_int4: null buffer");

@@ -31,6 +31,16 @@ KernelEvents take_kernel_events();
 // its last kernel).
 void arm_kernel_events(KernelEvents ev);
 
+// Placed first in every entry point that may launch: whatever path the call
+// leaves by (an argument error, an empty shape, a failed launch), events armed
+// for it do not stay armed for a later, unrelated call.
+struct DisarmOnExit {
+  DisarmOnExit() = default;
+  DisarmOnExit(const DisarmOnExit&) = delete;
+  DisarmOnExit& operator=(const DisarmOnExit&) = delete;
+  ~DisarmOnExit() { take_kernel_events(); }
+};
+
 // Every kernel of the library is launched through here.  With events armed the
 // launch goes through hipExtLaunchKernel, which stamps the kernel's own start
 // and end into them (a kernel trace's duration, without event markers around

@@ -76,6 +76,7 @@ int dscq_matmul_noalloc(const uint8_t* a, const uint8_t* b, const float* sx,
                         const void* bias, int64_t M, int64_t N, int64_t KP, int fused,
                         int force_decode, int out_fp32, void* out, int32_t* raw,
                         void* stream) {
+  DisarmOnExit disarm;
   // The argument checks of dscq_matmul (kernel/w4a4.cu:197).
   if (!(M > 0 && M <= 65535 && N > 0 && KP > 0 && KP <= 1048576 && KP % 64 == 0))
     return fail("Invalid dimensions");

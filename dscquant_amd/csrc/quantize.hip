@@ -380,8 +380,10 @@ __global__ __launch_bounds__(TPB) void row_quant_kernel(RowArgs a) {
     // it): one store instruction per iteration instead of four 4-byte pieces
     // per lane, and whole 64-byte segments leave the CU.  Measured: M = 2048,
     // K = 4096 5.52 -> 4.33 MB written, 7.57 -> 7.45 us; 4096 x 28672 59.5 ->
-    // 55.4 us.  A wave reads back only what it wrote; its LDS accesses
-    // complete in order.
+    // 55.4 us.  A wave reads back only what its own lanes wrote; the
+    // wave-scope release/acquire fence orders the other lanes' writes before
+    // the reads in the memory model (the wave's LDS accesses complete in
+    // order, so it costs at most a wait for them).
     __shared__ uint32_t pstage[TPB / 64][ITERS][256];
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
@@ -390,6 +392,8 @@ __global__ __launch_bounds__(TPB) void row_quant_kernel(RowArgs a) {
       for (int j = 0; j < 4; ++j)
         pstage[wave][it][(lane >> 2) * 16 + j * 4 + r] = packed_nibbles(ev[it][j], od[it][j]);
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       if (!FULL && !(wlive[it] || !real)) continue;

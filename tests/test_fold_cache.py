@@ -157,3 +157,67 @@ def test_non_w4a4_path_refuses_gradients():
     x = torch.randn(2, 16, requires_grad=True)
     with pytest.raises(RuntimeError, match="no gradient"):
         q(x)
+
+
+def test_fold_follows_module_casts():
+    """Module.half() swaps each parameter's .data (same object, same version):
+    the cached fold and clip values must follow the new dtype."""
+    rot = _LearnedRotation(2, 8)
+    lin = _linear(16, 24, seed=9)
+    q = QuantLinear(lin, None, rot, "v")
+    with torch.no_grad():
+        w1, b1 = q.transformed()
+    assert w1.dtype == torch.float32
+    q.half()
+    assert lin.weight.dtype == torch.float16
+    with torch.no_grad():
+        w2, b2 = q.transformed()
+    assert w2.dtype == torch.float16 and b2.dtype == torch.float16
+    assert q.clip_value("weight_clip") == 1.0
+    q.float()
+    with torch.no_grad():
+        w3, _ = q.transformed()
+    assert w3.dtype == torch.float32 and w3 is not w1
+
+
+def test_clip_value_follows_module_casts():
+    q = QuantLinear(_linear(8, 16, seed=10), None)
+    assert q.clip_value("activation_clip") == 1.0
+    q.activation_clip.data = torch.tensor(0.75)  # what Module._apply does per parameter
+    assert q.clip_value("activation_clip") == 0.75
+
+
+class _W4A4:
+    weight_bits, activation_bits = 4, 4
+
+
+@pytest.mark.parametrize("lead", [(0,), (3, 0), (0, 5)])
+@pytest.mark.parametrize("rotate", [0, 128])
+def test_empty_batch_returns_empty_output_without_launching(monkeypatch, lead, rotate):
+    """F.linear of an empty batch is an empty [..., 0, N] tensor in x's dtype
+    (core/linear.py:48-52); the integer path returns it without a library call."""
+    from dscquant_amd import _lib
+
+    def no_call(*a, **k):
+        raise AssertionError("library called for an empty batch")
+    monkeypatch.setattr(_lib, "call", no_call)
+    q = QuantLinear(_linear(32, 256, seed=11), _W4A4())
+    q.enabled, q.rotate_block = True, rotate
+    for dtype in (torch.float16, torch.float32):
+        x = torch.empty(*lead, 256, dtype=dtype)
+        with torch.no_grad():
+            y = q(x)
+        assert y.shape == (*lead, 32) and y.dtype == dtype
+
+
+def test_feature_mismatch_raises_like_f_linear(monkeypatch):
+    """K inside the same 64-element padding step as the weight's K would pass the
+    packed-shape checks; the module rejects it as F.linear does."""
+    from dscquant_amd import _lib
+    monkeypatch.setattr(_lib, "call", lambda *a, **k: (_ for _ in ()).throw(AssertionError()))
+    q = QuantLinear(_linear(32, 256, seed=12), _W4A4())
+    q.enabled = True
+    for shape in [(4, 250), (0, 250), (2, 3, 260)]:
+        with pytest.raises(RuntimeError, match="cannot be multiplied"):
+            with torch.no_grad():
+                q(torch.zeros(*shape, dtype=torch.float16))

@@ -216,3 +216,21 @@ def test_quant_mlp_non_fp16_inputs_run_the_composition(gpu, monkeypatch, dtype):
 
     assert torch.equal(g.cpu(), ref(gate, x)) and torch.equal(u.cpu(), ref(up, x))
     assert torch.equal(y.cpu(), ref(down, h))
+
+
+@pytest.mark.parametrize("lead", [(0,), (2, 0)])
+@pytest.mark.parametrize("rot,bias", [(0, False), (128, True)])
+def test_quant_linear_empty_batch(gpu, lead, rot, bias):
+    """An empty batch gives an empty [..., 0, N] output in x's dtype, as F.linear
+    does (core/linear.py:48-52), and a following forward is unaffected."""
+    K, N = 512, 256
+    q = QuantLinear(_base(N, K, 3, gpu, bias=bias), Cfg())
+    _enabled(q, rot=rot)
+    with torch.no_grad():
+        y = q(torch.empty(*lead, K, dtype=torch.float16, device=gpu))
+        assert y.shape == (*lead, N) and y.dtype == torch.float16 and y.device == gpu
+        x = torch.from_numpy(activations(4, K, seed=5)).to(gpu)
+        y1 = q(x)
+        y2 = QuantLinear(q.base, Cfg())
+        _enabled(y2, rot=rot)
+        torch.testing.assert_close(y1, y2(x), rtol=0, atol=0)

@@ -189,6 +189,35 @@ def warm_up(step, seconds, torch):
 COPY_BYTES = 16 << 20
 
 
+def probes(torch, dev):
+    """Launchers of the measurement probes (include/dscq.h): a streaming kernel
+    with a kernel's own byte shape, and the MFMAs of a GEMM with no memory
+    traffic.  The ceilings reported beside the kernels they bound."""
+    from dscquant_amd import _lib
+    L = _lib.lib()
+    sink = torch.empty(4096, dtype=torch.int32, device=dev)
+
+    def stream(src, read_bytes, dst, write_bytes, pieces):
+        rc = L.dscq_stream_probe(src.data_ptr(), read_bytes,
+                                 (dst if dst is not None else sink).data_ptr(), write_bytes,
+                                 pieces, _lib.stream(dev))
+        assert rc == 0, L.dscq_last_error()
+
+    def mfma(M, N, K):
+        """The MFMA count of an M x N x K GEMM (2 M N K / 65536 per 32x32x32 MFMA)
+        spread over 256 workgroups of 8 waves; None if it does not divide evenly."""
+        total = M * N * K // 32768
+        if (M * N * K) % 32768 or total % (2048 * 8):
+            return None
+        per_wave = total // 2048
+
+        def launch(i):
+            rc = L.dscq_mfma_probe(256, 8, per_wave, sink.data_ptr(), _lib.stream(dev))
+            assert rc == 0, L.dscq_last_error()
+        return launch
+    return stream, mfma
+
+
 def kernel_class(name):
     if "row_quant" in name:
         # template arguments <T, ROT, MODE, ...>: MODE 1 is the weight pre-pack
@@ -449,9 +478,18 @@ def main():
             gemm()
         for i in range(args.kernel_iters):
             dst.copy_(srcs[i % len(srcs)])
+        stream_probe, mfma_probe = probes(torch, dev)
+        qdst = torch.empty((MP, KP // 2), dtype=torch.uint8, device=dev)
+        for i in range(args.kernel_iters):
+            stream_probe(xs[i % nbuf], 2 * M * K, qdst, M * K // 2, 4)
+        mfma_launch = mfma_probe(M, N, K)
+        if mfma_launch:
+            for i in range(args.kernel_iters):
+                mfma_launch(i)
         torch.cuda.synchronize()
         print(f"kernels-only: {args.kernel_iters} launches each of quantize, gemm, "
-              f"{COPY_BYTES >> 20} MiB copy", flush=True)
+              f"{COPY_BYTES >> 20} MiB copy, the quantize-shaped stream probe"
+              f"{' and the MFMA probe' if mfma_launch else ''}", flush=True)
         return
 
     # ---- per-kernel device times (HIP events on the launch stream): inside
@@ -462,6 +500,15 @@ def main():
     t_quant_iso = time_kernel(lambda i: quantize(xs[i % nbuf]), args.kernel_iters, torch, dev)
     quantize(xs[0])
     t_gemm_iso = time_kernel(lambda i: gemm(), args.kernel_iters, torch, dev)
+    # Ceilings, back to back in graphs like the isolated figures: a plain
+    # streaming kernel moving the quantize's bytes (read x, write M K / 2), and
+    # the GEMM's MFMAs alone (None where the count does not spread evenly).
+    stream_probe, mfma_probe = probes(torch, dev)
+    qdst = torch.empty((MP, KP // 2), dtype=torch.uint8, device=dev)
+    t_copy = (time_kernel(lambda i: stream_probe(xs[i % nbuf], 2 * M * K, qdst, M * K // 2, 4),
+                          args.kernel_iters, torch, dev) if (2 * M * K) % 64 == 0 else None)
+    mfma_launch = mfma_probe(M, N, K)
+    t_mfma = time_kernel(mfma_launch, args.kernel_iters, torch, dev) if mfma_launch else None
 
     # ---- whole steps.  Runs of up to GRAPH_STEPS consecutive steps are captured
     # into one HIP graph each, so the timed region is the GPU's own step time
@@ -531,7 +578,10 @@ def main():
                      "unit": "TFLOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "kernel": "w4a4_gemm_pipe_kernel", "avg_us": round(t_gemm * 1e6, 3),
                      "isolated_us": round(t_gemm_iso * 1e6, 3),
-                     "ops_per_launch": ops, "algorithmic_bytes": M * K // 2 + N * K // 2 + 2 * M * N}
+                     "ops_per_launch": ops, "algorithmic_bytes": M * K // 2 + N * K // 2 + 2 * M * N,
+                     "mfma_only_us": None if t_mfma is None else round(t_mfma * 1e6, 3),
+                     "mfma_only_frac": (None if t_mfma is None else
+                                        round(ops / t_mfma / 1e12 / PEAK_INT8_TOPS, 4))}
 
     traffic = load_traffic(args.workload)
     cpu = None
@@ -562,6 +612,9 @@ def main():
                          "unit": "GB/s", "frac": round(quant_gbs / PEAK_HBM_GBS, 4),
                          "avg_us": round(t_quant * 1e6, 3),
                          "isolated_us": round(t_quant_iso * 1e6, 3), "bytes_per_launch": qbytes,
+                         "copy_ceiling_us": None if t_copy is None else round(t_copy * 1e6, 3),
+                         "copy_ceiling_frac": (None if t_copy is None else
+                                               round(qbytes / t_copy / 1e9 / PEAK_HBM_GBS, 4)),
                          "traffic": (traffic["quantize"]["traffic"]
                                      if traffic and "quantize" in traffic else None)},
             "gemm": gemm_line,
@@ -694,6 +747,9 @@ def main_decode(args, torch, _lib, w4a4):
             step(i)
         for i in range(args.kernel_iters):
             dst.copy_(srcs[i % len(srcs)])
+        stream_probe, _ = probes(torch, dev)
+        for i in range(args.kernel_iters):
+            stream_probe(packs[i % nw][0], wbytes, None, 0, 4)
         torch.cuda.synchronize()
         print(f"kernels-only: {args.kernel_iters} steps ("
               f"{'fused decode kernel' if fused_ok else 'quantize + skinny-M GEMM'}), "
@@ -708,6 +764,11 @@ def main_decode(args, torch, _lib, w4a4):
     t_step = run_graph_steps(args, torch, dev, step)
     ops = 2.0 * M * N * K
     traffic = load_traffic(args.workload) or {}
+    # Ceiling: a bare read of the weight bytes the step streams (the best of
+    # 2, 4 or 8 pieces per thread), back to back in a graph.
+    stream_probe, _ = probes(torch, dev)
+    t_read = min(time_kernel(lambda i, p=p: stream_probe(packs[i % nw][0], wbytes, None, 0, p),
+                             args.kernel_iters, torch, dev) for p in (2, 4, 8))
 
     def hbm_line(kernel, dbytes, t, cls, t_iso=None):
         gbs = dbytes / t / 1e9
@@ -755,7 +816,9 @@ def main_decode(args, torch, _lib, w4a4):
         "config": {"workload": f"{args.workload}: W4A4 linear M={M} K={K} N={N}, rotate_block="
                                f"{rot}, {how}, {nw} weight sets cycled (HBM-resident)",
                    "M": M, "N": N, "K": K, "rotate_block": rot, "weight_sets": nw},
-        "roofline": line,
+        "roofline": dict(line, read_ceiling_us=round(t_read * 1e6, 3),
+                         read_ceiling_bytes=wbytes,
+                         read_ceiling_frac=round(wbytes / t_read / 1e9 / PEAK_HBM_GBS, 4)),
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

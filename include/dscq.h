@@ -269,6 +269,40 @@ int dscq_device_supported(void);
  */
 int dscq_time_next_kernel(void* start, void* stop);
 
+/*
+ * Measurement probes (no reference counterpart): the ceilings the kernels
+ * above are compared against, timed on the same device in the same run (with
+ * dscq_time_next_kernel like any other call).
+ *
+ * dscq_stream_probe: a plain streaming kernel.  Each thread reads `pieces`
+ * (1, 2, 4, 8 or 16) 16-byte pieces of `src`, thread t the pieces t + j * T
+ * (T = read_bytes / (16 * pieces) threads, so each load instruction of a wave
+ * reads 1 KiB contiguous), and
+ *   write_bytes == read_bytes / pieces: writes their XOR to dst piece t
+ *     (with pieces = 4 over fp16 input: exactly the bytes of an activation
+ *     quantize, read 2 M K and write M K / 2);
+ *   write_bytes == 0: writes nothing (a bare read; dst, 16 bytes, receives a
+ *     piece only if some thread's pieces XOR to a fixed 128-bit constant).
+ * src and dst 16-byte aligned; read_bytes a positive multiple of 16 * pieces.
+ */
+int dscq_stream_probe(const void* src, int64_t read_bytes, void* dst, int64_t write_bytes,
+                      int pieces, void* stream);
+
+/*
+ * dscq_mfma_probe: the matrix cores alone.  `workgroups` workgroups of `waves`
+ * (1..8) waves; each wave issues `mfmas_per_wave` (a multiple of 8)
+ * v_mfma_i32_32x32x32_i8 on register operands, four per step over a 2 x 2
+ * block of accumulators (a pipelined-GEMM wave's step), with no memory
+ * traffic in the loop, alternating two operand sets.  Operand bytes vary over
+ * lanes and bytes (multiples of 16 in [-128, 96], as unpacked int4 operands);
+ * out[workgroup * waves + wave] (int32) receives the wave's wrapping sum of all
+ * its accumulator elements, a closed form of the operand values that does not
+ * depend on the operand layout (the checksum the GPU tests recompute).  256 workgroups of 8 waves and 512 MFMAs per
+ * wave are the 2 M N K operations of a 2048 x 4096 x 4096 GEMM.
+ */
+int dscq_mfma_probe(int64_t workgroups, int waves, int64_t mfmas_per_wave, int32_t* out,
+                    void* stream);
+
 /* Message of the last DSCQ_EINVAL / launch failure on this thread. */
 const char* dscq_last_error(void);
 

@@ -129,6 +129,17 @@ def test_c_other_argument_checks():
                                         d, d, d, None, None)
 
 
+def test_c_probe_argument_checks():
+    d = 16
+    assert "pieces" in _einval("dscq_stream_probe", d, 64, d, 16, 3, None)
+    assert "multiple" in _einval("dscq_stream_probe", d, 48, d, 0, 4, None)
+    assert "write_bytes" in _einval("dscq_stream_probe", d, 256, d, 32, 4, None)
+    assert "aligned" in _einval("dscq_stream_probe", 8, 256, d, 64, 4, None)
+    assert "waves" in _einval("dscq_mfma_probe", 4, 9, 64, d, None)
+    assert "multiple of 8" in _einval("dscq_mfma_probe", 4, 8, 12, d, None)
+    assert "workgroups" in _einval("dscq_mfma_probe", 0, 8, 64, d, None)
+
+
 def test_c_linear_decode_limits_and_checks():
     L = _lib.lib()
     # One 128-element block per quad of a 512-lane workgroup: M * ceil(KP/128) <= 128.

@@ -81,6 +81,9 @@ def parse():
                    help="run the workload's steps back to back this long before timing anything "
                         "(from idle the GPU takes a few hundred milliseconds to reach its "
                         "steady clock)")
+    p.add_argument("--gemm-kernel", choices=("auto", "wide", "pipe"), default="auto",
+                   help="dense GEMM kernel (dscq_set_gemm_kernel): the automatic choice, the "
+                        "wide-tile kernel wherever it applies, or never the wide-tile kernel")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-graph", action="store_true")
     p.add_argument("--kernels-only", action="store_true",
@@ -223,13 +226,22 @@ def kernel_class(name):
         # template arguments <T, ROT, MODE, ...>: MODE 1 is the weight pre-pack
         args = name.split("row_quant_kernel<", 1)[-1].split(",")
         return "pack" if len(args) > 2 and args[2].strip() == "1" else "quantize"
-    if "w4a4_gemm" in name or "w4a4_gemv" in name:
+    if "w4a4_gemm" in name or "w4a4_gemv" in name:  # pipe, wide, general kernels
         return "gemm"
     if "w4a4_decode" in name:
         return "decode"
     if "copy" in name.lower():
         return "copy"
     return None
+
+
+def gemm_kernel_name(M, N, K, choice, cus=256):
+    """The dense kernel dscq_matmul takes for an fp16 M x N x K GEMM at M >= 64
+    outside the skinny-M range (the library's dispatch rule, restated)."""
+    fits = N % 8 == 0 and K % 256 == 0 and K <= 65536 and M >= 64
+    t256 = -(-M // 256) * -(-N // 256)
+    wide = fits and choice != "pipe" and (choice == "wide" or (M >= 256 and t256 >= 2 * cus))
+    return "w4a4_gemm_wide_kernel" if wide else "w4a4_gemm_pipe_kernel"
 
 
 def traffic_summary(fetch_csv, write_csv):
@@ -420,6 +432,7 @@ def main():
     import torch
     from dscquant_amd import _lib, w4a4
 
+    _lib.lib().dscq_set_gemm_kernel({"auto": 0, "wide": 1, "pipe": 2}[args.gemm_kernel])
     if args.workload == "mlp":
         return main_mlp(args, torch, _lib, w4a4)
     if args.workload.startswith("decode"):
@@ -500,15 +513,22 @@ def main():
     t_quant_iso = time_kernel(lambda i: quantize(xs[i % nbuf]), args.kernel_iters, torch, dev)
     quantize(xs[0])
     t_gemm_iso = time_kernel(lambda i: gemm(), args.kernel_iters, torch, dev)
-    # Ceilings, back to back in graphs like the isolated figures: a plain
-    # streaming kernel moving the quantize's bytes (read x, write M K / 2), and
-    # the GEMM's MFMAs alone (None where the count does not spread evenly).
+    # Ceilings, each timed in the step in place of the kernel it bounds (like
+    # the kernels' own in-step figures): a plain streaming kernel moving the
+    # quantize's bytes (read x, write M K / 2) between GEMMs, and the GEMM's
+    # MFMAs alone (None where the count does not spread evenly) after quantizes.
     stream_probe, mfma_probe = probes(torch, dev)
     qdst = torch.empty((MP, KP // 2), dtype=torch.uint8, device=dev)
-    t_copy = (time_kernel(lambda i: stream_probe(xs[i % nbuf], 2 * M * K, qdst, M * K // 2, 4),
-                          args.kernel_iters, torch, dev) if (2 * M * K) % 64 == 0 else None)
+    t_copy = None
+    if (2 * M * K) % 64 == 0:
+        t_copy = time_in_steps(
+            [lambda i: stream_probe(xs[i % nbuf], 2 * M * K, qdst, M * K // 2, 4),
+             lambda i: gemm()], args.kernel_iters, torch)[0]
     mfma_launch = mfma_probe(M, N, K)
-    t_mfma = time_kernel(mfma_launch, args.kernel_iters, torch, dev) if mfma_launch else None
+    t_mfma = None
+    if mfma_launch:
+        t_mfma = time_in_steps([lambda i: quantize(xs[i % nbuf]), mfma_launch],
+                               args.kernel_iters, torch)[1]
 
     # ---- whole steps.  Runs of up to GRAPH_STEPS consecutive steps are captured
     # into one HIP graph each, so the timed region is the GPU's own step time
@@ -576,7 +596,8 @@ def main():
     else:
         gemm_line = {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
-                     "kernel": "w4a4_gemm_pipe_kernel", "avg_us": round(t_gemm * 1e6, 3),
+                     "kernel": gemm_kernel_name(M, N, K, args.gemm_kernel),
+                     "avg_us": round(t_gemm * 1e6, 3),
                      "isolated_us": round(t_gemm_iso * 1e6, 3),
                      "ops_per_launch": ops, "algorithmic_bytes": M * K // 2 + N * K // 2 + 2 * M * N,
                      "mfma_only_us": None if t_mfma is None else round(t_mfma * 1e6, 3),
@@ -603,7 +624,7 @@ def main():
         "data": "synthetic: X~N(0,1) fp16 with 1% outlier channels x50, W~N(0,0.02), seeded",
         "config": {"workload": f"{args.workload}: W4A4 linear M={M} K={K} N={N}, "
                                f"rotate_block={rot}, pre-packed weights, fp16 out",
-                   "M": M, "N": N, "K": K, "rotate_block": rot,
+                   "M": M, "N": N, "K": K, "rotate_block": rot, "gemm_kernel": args.gemm_kernel,
                    "input_buffers": nbuf, "steps_per_graph": None if args.no_graph else GRAPH_STEPS},
         "roofline": dict(gemm_line, traffic=(traffic["gemm"]["traffic"]
                                              if traffic and "gemm" in traffic else None)),

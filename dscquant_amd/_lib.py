@@ -42,6 +42,7 @@ SIGNATURES = {
     "dscq_pack_int4": [_P, _I64, _I64, _P, _P],
     "dscq_unpack_int4": [_P, _I64, _I64, _I64, _P, _P],
     "dscq_time_next_kernel": [_P, _P],
+    "dscq_set_gemm_kernel": [_I],
     "dscq_stream_probe": [_P, _I64, _P, _I64, _I, _P],
     "dscq_mfma_probe": [_I64, _I, _I64, _P, _P],
     "dscq_device_supported": [],

@@ -9,6 +9,7 @@
 
 #include "../../include/dscq.h"
 #include "common.h"
+#include "gemm_args.h"
 
 namespace dscq {
 
@@ -42,7 +43,10 @@ int linear_decode(const void* x, int dtype, int64_t M, int64_t K, float clip, in
 namespace {
 thread_local char g_last_error[512] = "";
 thread_local KernelEvents g_kernel_events = {nullptr, nullptr};
+thread_local int g_gemm_kernel = 0;
 }  // namespace
+
+int gemm_kernel_preference() { return g_gemm_kernel; }
 
 KernelEvents take_kernel_events() {
   const KernelEvents ev = g_kernel_events;
@@ -110,6 +114,13 @@ const char* dscq_version(void) { return "dscq 0.2.0 (gfx950)"; }
 int dscq_time_next_kernel(void* start, void* stop) {
   g_kernel_events = {static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)};
   return DSCQ_OK;
+}
+
+int dscq_set_gemm_kernel(int which) {
+  if (which < 0 || which > 2) return fail("set_gemm_kernel: 0, 1 or 2 (got %d)", which);
+  const int prev = g_gemm_kernel;
+  g_gemm_kernel = which;
+  return prev;
 }
 
 int dscq_device_supported(void) {

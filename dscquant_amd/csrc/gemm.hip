@@ -45,33 +45,13 @@
 
 #include "../../include/dscq.h"
 #include "common.h"
+#include "gemm_args.h"
 #include "mma_int4.h"
 #include "rowquant.h"
 
 namespace dscq {
 namespace {
 
-struct GemmArgs {
-  const uint8_t* a;
-  const uint8_t* b;
-  const float* sx;
-  const int32_t* zx;
-  const float* sw;
-  const int32_t* sums;
-  const void* bias;  // null or [N] of the output type
-  void* out;         // [M, N] fp16 or fp32
-  int32_t* raw;      // null or [M, N]
-  int64_t M, N, KP;
-  int64_t arows, brows;  // readable rows of a (>= MP) and b (>= NP)
-  int tiles_n;
-  // K split over workgroups (pipelined kernel only): part p of every tile
-  // covers 256-nibble slices [p * kslices, (p + 1) * kslices) and writes its
-  // int32 sums to part + p * M * N; a second pass adds the parts and applies
-  // the epilogue.
-  int32_t* part = nullptr;
-  int kslices = 0;
-  int tiles = 0;  // tiles per part
-};
 
 constexpr int kSliceBytes = 64;  // 128 nibbles of K per LDS stage
 constexpr int kPlanePad = 64;
@@ -1077,6 +1057,17 @@ bool use_pipe_mid_m(const GemmArgs& g, bool gated = false) {
          pipe_layout_ok(g);
 }
 
+// The wide-tile kernel (gemm_wide.hip) for fp16 output without raw
+// accumulators when its 256 x 256 tiles make at least two rounds of one tile
+// per CU (or wherever it applies, or never: dscq_set_gemm_kernel).
+bool use_wide(const GemmArgs& g, bool out_half) {
+  const int pref = gemm_kernel_preference();
+  if (pref == 2 || !out_half || g.M < 64 || !wide_gemm_fits(g)) return false;
+  if (pref == 1) return true;
+  const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 255) / 256);
+  return g.M >= 256 && t256 >= 2 * cu_count();
+}
+
 template <typename OutT>
 int gemm_typed(const GemmArgs& g, bool decode, int32_t* ws, int64_t ws_bytes,
                hipStream_t stream) {
@@ -1097,6 +1088,9 @@ int gemm_typed(const GemmArgs& g, bool decode, int32_t* ws, int64_t ws_bytes,
   // M = 64..160 6.1-7.5 us against 11.1 us; N = 2048, M = 64..96 6.3-7.5 us
   // against 11.3 us; N = 4096, M = 64 9.3 against 11.4 us, M = 96 13.0 against
   // 11.2 us).  Shorter rows keep the pipelined kernel (not measured there).
+  // (The wide-tile kernel's own rule never meets the skinny one; checked
+  // first so that a forced choice covers every M >= 64.)
+  if (use_wide(g, sizeof(OutT) == 2)) return launch_wide_gemm(g, stream);
   if (g.KP >= 4096 && g.KP <= 65536 && (g.M + 15) / 16 * g.N <= 16384)
     return launch_gemv<OutT>(g, stream);
   if (g.KP > 65536) return launch_cfg<OutT, 64, 64, 2, 2, true>(g, stream);
@@ -1106,10 +1100,11 @@ int gemm_typed(const GemmArgs& g, bool decode, int32_t* ws, int64_t ws_bytes,
   return launch_cfg<OutT, 128, 128, 2, 2, false>(g, stream);
 }
 
-// Whether gemm_typed takes the pipelined kernel.
-bool takes_pipe(const GemmArgs& g, bool decode) {
+// Whether gemm_typed takes the pipelined kernel (the one that may split K).
+bool takes_pipe(const GemmArgs& g, bool decode, bool out_half) {
   if (decode || g.M <= 16) return false;
   if (g.M < 64) return use_pipe_mid_m(g);
+  if (use_wide(g, out_half)) return false;
   if (g.KP >= 4096 && g.KP <= 65536 && (g.M + 15) / 16 * g.N <= 16384) return false;
   if (g.KP > 65536) return false;
   return pipe_ok(g);
@@ -1131,7 +1126,9 @@ int64_t w4a4_gemm_workspace_bytes(int64_t M, int64_t N, int64_t KP, bool decode)
   g.arows = ceil_to(M, 8);
   g.brows = ceil_to(N, 8);
   g.tiles_n = 0;
-  return takes_pipe(g, decode) ? split_workspace_bytes(g) : 0;
+  // The query has no output dtype: shapes the wide-tile kernel takes (fp16)
+  // make so many tiles that the pipelined kernel would not split them either.
+  return takes_pipe(g, decode, false) ? split_workspace_bytes(g) : 0;
 }
 
 int w4a4_gemm(const uint8_t* a, const uint8_t* b, const float* sx, const int32_t* zx,

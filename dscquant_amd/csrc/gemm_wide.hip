@@ -1,0 +1,399 @@
+// Wide-tile W4A4 GEMM for gfx950: 256 x 256 output tiles, one workgroup of
+// four waves per CU (one wave per SIMD), each wave a 128 x 128 block of 4 x 4
+// v_mfma_i32_32x32x32_i8 tiles whose 256 accumulator registers live in AGPRs.
+//
+// Semantics as gemm.hip (kernel/w4a4.cu:70-161): both operands are packed
+// int4, K-contiguous; nibbles are unpacked to int8 (x16) in registers
+// (mma_int4.h), so the int32 sums carry a factor 256.
+//
+// Data moved per multiply-accumulate, against the pipelined kernel's 256 x 128
+// tile of eight 64 x 64 waves: per MFMA a wave reads half a 16-byte fragment
+// from LDS (8 fragments feed 16 MFMAs per k-step) instead of one, and spends 3
+// VALU instructions on unpacking instead of 6; the tile loads (256 + 256) rows
+// per 65536 outputs instead of (256 + 128) per 32768, a third fewer bytes.
+//
+// K advances in 256-nibble slices: 128 bytes of every A and B row of the tile,
+// 64 KiB per slice, double-buffered in LDS.  Global memory reaches LDS by DMA
+// (global_load_lds_dwordx4, 16 bytes per lane written straight to LDS, no
+// register staging): instruction j of wave w fills 8 rows, 8d .. 8d + 7 of the
+// tile's 512 (d = 16 w + j: A rows 0-255 from waves 0-1, B rows from waves
+// 2-3); lane l writes position l % 8 of row 8d + l / 8, so it loads the row's
+// 16-byte unit (l % 8) ^ ((row >> 1) & 7): the pipelined kernel's swizzle,
+// applied on the global side, which keeps the fragment reads conflict-free.
+//
+// Schedule of slice s (LDS stage c = s & 1), k-steps 0..7 of 16 MFMAs each;
+// every step interleaves its MFMAs with the unpack of the next step:
+//   steps 1, 3   fragment units q = 2, 3 of slice s read from stage c
+//   before 5     this wave's DMA of slice s + 1 waited for (vmcnt), then a
+//                barrier: slice s + 1 is in stage c ^ 1 for every wave, and
+//                every wave's reads of stage c for slice s are complete
+//   step 5       unit q = 0 of slice s + 1 read; the DMA of slice s + 2 into
+//                stage c issued, a whole slice before the barrier that needs it
+//   step 7       unit q = 1 of slice s + 1 read
+// Each unit is read two steps before the first unpack that uses it, so no more
+// than two units' fragments (64 registers) are held at once.
+// Lane l of a fragment read takes row l % 32, unit 2q + l / 32 (stored at
+// (2q + l / 32) ^ ((row >> 1) & 7)): its low 8 bytes feed k-step 2q, the high
+// 8 bytes k-step 2q + 1, the same for A and B, so every product pairs equal k.
+//
+// Epilogue: the scale and zero-point factors are staged pre-multiplied, sx / 256
+// and (8 - zx) * 256, so corrected * 256 = acc + (8 - zx) * 256 * sums is one
+// v_mad_i32_i24 and float(corrected * 256) * (sx / 256) equals
+// float(corrected) * sx exactly (power-of-two scalings, no overflow: |acc| <=
+// 2^30 and |corrected| < 2^23 for K <= 65536); then * sw (+ bias) and one fp16
+// rounding (v_cvt_pk_f16_f32), the reference's operation order.  Each wave's
+// 128 x 128 fp16 tile goes through LDS (the idle slice stages) so that every
+// store instruction writes four whole 256-byte row segments.
+
+#include <type_traits>
+
+#include "../../include/dscq.h"
+#include "common.h"
+#include "gemm_args.h"
+#include "mma_int4.h"
+
+namespace dscq {
+namespace {
+
+constexpr int kTile = 256;                    // rows of A and of B per tile
+constexpr int kSlice = 128;                   // bytes of a packed row per slice
+constexpr int kHalf = kTile * kSlice;         // 32 KiB: one operand's rows of a slice
+constexpr int kStage = 2 * kHalf;             // 64 KiB per slice
+// LDS: A of stage 0, A of stage 1, B of stage 0, B of stage 1 (32 KiB each),
+// so that every fragment of either stage is within a ds_read immediate offset
+// (< 64 KiB) of one A base and one B base per unit.
+constexpr int kBRegion = 2 * kHalf;
+constexpr int kWaves = 4;
+constexpr int kDma = 2 * kTile / 8 / kWaves;  // DMA instructions (8 rows each) per wave per slice
+
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land
+// at LDS byte address lds + 16 l (lds wave-uniform, through M0).  Inline
+// assembly, so that the compiler's wait-count pass does not treat LDS reads
+// as waiting on it; the kernel waits for these loads itself (vmcnt) before the
+// barrier that publishes their data.  M0 is a reserved register, which clang
+// warns about on a clobber list: nothing else in this kernel uses it on gfx950
+// (its LDS instructions take no M0), as its assembly shows.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <bool BIAS>
+__global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs g) {
+  constexpr int FM = 4, FN = 4, NF = FM + FN;  // 128 x 128 per wave
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStage + kTile * 20];
+  float* const lds_sx = reinterpret_cast<float*>(smem + 2 * kStage);            // sx / 256
+  int32_t* const lds_z = reinterpret_cast<int32_t*>(smem + 2 * kStage + kTile * 4);  // (8 - zx) * 256
+  float* const lds_sw = reinterpret_cast<float*>(smem + 2 * kStage + kTile * 8);
+  int32_t* const lds_sum = reinterpret_cast<int32_t*>(smem + 2 * kStage + kTile * 12);
+  float* const lds_b = reinterpret_cast<float*>(smem + 2 * kStage + kTile * 16);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tile_m = (int)(blockIdx.x / (unsigned)g.tiles_n);
+  const int tile_n = (int)(blockIdx.x % (unsigned)g.tiles_n);
+  const int64_t m0 = (int64_t)tile_m * kTile, n0 = (int64_t)tile_n * kTile;
+  const int64_t KB = g.KP / 2;
+  const int nslices = (int)(KB / kSlice);
+
+  // ---- DMA sources.  Instruction j of this wave covers the 8 tile rows
+  // 8d .. 8d + 7 (d = 16 wave + j) of A (waves 0-1) or B (waves 2-3); the
+  // tile origin and MP / NP are multiples of 8, so a group is wholly inside
+  // the operand's rows or wholly past them, and groups past them are clamped
+  // to its last 8 rows (their sums are never stored): a wave-uniform base per
+  // instruction.  Lane l reads row 8d + l / 8 at unit (l % 8) ^ ((row >> 1) & 7),
+  // and (row >> 1) & 7 = (4 (j % 2) + l / 16) % 8, so the per-lane offset
+  // depends on the parity of j only.
+  const bool a_side = wave < 2;
+  const uint8_t* const dbase = a_side ? g.a : g.b;
+  const int64_t rows_end = (a_side ? g.arows : g.brows) - 8;
+  const int64_t r0 = a_side ? m0 : n0 - kTile;  // operand row of tile row 0
+  const uint8_t* gbase[kDma];                    // wave-uniform: scalar registers
+#pragma unroll
+  for (int j = 0; j < kDma; ++j) gbase[j] = dbase + min(r0 + 8 * (kDma * wave + j), rows_end) * KB;
+  uint32_t lane_off[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+    lane_off[p] = (uint32_t)((lane >> 3) * KB + 16 * ((lane & 7) ^ ((4 * p + (lane >> 4)) & 7)));
+  // LDS destination of this wave's rows: its operand's region, rows
+  // (wave % 2) * 128 .. +127 of the tile.
+  const uint32_t lds_dma = (uint32_t)__builtin_amdgcn_readfirstlane(
+      (int)((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem +
+            (uint32_t)((a_side ? 0 : kBRegion) + (wave & 1) * 128 * kSlice)));
+  // Instruction j of slice `slice` into `stage`; the slice offset rides on the
+  // per-lane offsets (off[p] = lane_off[p] + slice * 128), the bases stay put.
+  auto dma_one = [&](int j, const uint32_t (&off)[2], int stage) {
+    dma16(gbase[j], off[j & 1], lds_dma + (uint32_t)(stage * kHalf + j * 8 * kSlice));
+  };
+  auto dma = [&](int slice, int stage) {
+    const uint32_t off[2] = {lane_off[0] + (uint32_t)slice * kSlice,
+                             lane_off[1] + (uint32_t)slice * kSlice};
+#pragma unroll
+    for (int j = 0; j < kDma; ++j) dma_one(j, off, stage);
+  };
+
+  // ---- fragment reads: per unit q one A base and one B base (stage 0,
+  // fragment 0); the stage and the fragment are immediate offsets.
+  const int fr = lane & 31;
+  const int fsw = (fr >> 1) & 7;
+  uint32_t abase[4], bbase[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t qo = 16 * ((2 * q + (lane >> 5)) ^ fsw);
+    abase[q] = (uint32_t)((wm * 128 + fr) * kSlice) + qo;
+    bbase[q] = (uint32_t)(kBRegion + (wn * 128 + fr) * kSlice) + qo;
+  }
+  uint4 P[4][NF];
+  auto lread = [&](int stage, int q) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint32_t off = f < FM ? abase[q] + (uint32_t)(stage * kHalf + f * 32 * kSlice)
+                                  : bbase[q] + (uint32_t)(stage * kHalf + (f - FM) * 32 * kSlice);
+      P[q][f] = *reinterpret_cast<const uint4*>(smem + off);
+    }
+  };
+
+  // Accumulators: the first MFMA of each takes a literal zero as its C operand
+  // (slice 0's first step, peeled), so no registers are ever zero-filled --
+  // a zero-filled accumulator array is 256 VGPRs that only then move to AGPRs.
+  v16i acc[FM][FN];
+  v4i U0[NF], U1[NF];
+  // k-step t of a slice uses P[t / 2] dwords (2 * (t % 2), +1).
+  auto unpack_step = [&](v4i (&U)[NF], int t) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint4 w = P[t >> 1][f];
+      U[f] = (t & 1) ? unpack8(w.z, w.w) : unpack8(w.x, w.y);
+    }
+  };
+  // B first: acc[i][j] accumulates the transposed 32 x 32 tile.
+  auto mfma_step = [&](const v4i (&U)[NF]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(U[FM + j], U[i], acc[i][j], 0, 0, 0);
+  };
+  auto mfma_first = [&](const v4i (&U)[NF]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(U[FM + j], U[i], v16i{0}, 0, 0, 0);
+  };
+  // Half h of fragment f of k-step t (3 VALU: two unpacked dwords).
+  auto unpack_half = [&](v4i (&U)[NF], int t, int f, int h) {
+    const uint4 w = P[t >> 1][f];
+    const uint32_t x = (t & 1) ? (h ? w.w : w.z) : (h ? w.y : w.x);
+    U[f][2 * h] = (int)((x << 4) & 0xF0F0F0F0u);
+    U[f][2 * h + 1] = (int)(x & 0xF0F0F0F0u);
+  };
+  // One MFMA, then three of the step's unpack VALU instructions, and so on.
+  auto interleave = [&]() {
+#pragma unroll
+    for (int k = 0; k < FM * FN; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ---- prologue: slice 0 and the tile's row / column metadata, then slice 1.
+  dma(0, 0);
+  const int64_t mrow = min(m0 + tid, g.arows - 1), ncol = min(n0 + tid, g.brows - 1);
+  const float meta_sx = g.sx[mrow];
+  const int32_t meta_z = g.zx[mrow];
+  const float meta_sw = g.sw[ncol];
+  const int32_t meta_sum = g.sums[ncol];
+  const float meta_b =
+      BIAS ? __half2float(static_cast<const __half*>(g.bias)[min(n0 + tid, g.N - 1)]) : 0.0f;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // slice 0 and the metadata
+  lds_sx[tid] = meta_sx * 0.00390625f;                // exact: a power-of-two scaling
+  lds_z[tid] = (8 - meta_z) * 256;
+  lds_sw[tid] = meta_sw;
+  lds_sum[tid] = meta_sum;
+  if (BIAS) lds_b[tid] = meta_b;
+  if (nslices > 1) dma(1, 1);
+  barrier_lds();
+  lread(0, 0);
+  lread(0, 1);
+  unpack_step(U0, 0);
+
+  // The barrier and the reads of the next slice's first units run after the
+  // last slice too (they read a stage nothing uses any more, and the unpack
+  // result is dropped), so one body serves every slice; only the DMA of slice
+  // s + 2 depends on whether it exists (a uniform branch between two steps).
+  auto slice = [&](int s, auto stage, auto first) {
+    constexpr int C = decltype(stage)::value, NX = C ^ 1;
+    if constexpr (decltype(first)::value)
+      mfma_first(U0);
+    else
+      mfma_step(U0);
+    unpack_step(U1, 1);
+    interleave();
+    mfma_step(U1);
+    unpack_step(U0, 2);
+    lread(C, 2);
+    interleave();
+    mfma_step(U0);
+    unpack_step(U1, 3);
+    interleave();
+    mfma_step(U1);
+    unpack_step(U0, 4);
+    lread(C, 3);
+    interleave();
+    mfma_step(U0);
+    unpack_step(U1, 5);
+    interleave();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of slice s + 1
+    barrier_lds();
+    lread(NX, 0);
+    // Step 5 by hand: sixteen groups of one MFMA, three unpack instructions
+    // of step 6 and one DMA instruction, so the loads issue in the MFMAs'
+    // shadow instead of in a burst before them.  The DMA is unconditional
+    // (no branch around MFMA code, whose accumulators would be copied at the
+    // join): in the last two slices it reloads the last slice into stage c,
+    // whose reads all completed before the barrier above; the epilogue waits
+    // for it before it reuses the stages.
+    {
+      const uint32_t sl = (uint32_t)min(s + 2, nslices - 1) * kSlice;
+      const uint32_t off[2] = {lane_off[0] + sl, lane_off[1] + sl};
+#pragma unroll
+      for (int k = 0; k < FM * FN; ++k) {
+        const int i = k / FN, j = k % FN;
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(U1[FM + j], U1[i], acc[i][j], 0, 0, 0);
+        unpack_half(U0, 6, k / 2, k % 2);
+        dma_one(k, off, C);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    mfma_step(U0);
+    unpack_step(U1, 7);
+    interleave();
+    mfma_step(U1);
+    unpack_step(U0, 0);
+    lread(NX, 1);
+    interleave();
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  slice(0, S0{}, std::true_type{});
+  for (int s = 1; s < nslices; s += 2) {
+    slice(s, S1{}, std::false_type{});
+    if (s + 1 < nslices) slice(s + 1, S0{}, std::false_type{});
+  }
+
+  // ---- epilogue.  acc[i][j] is the transposed tile: output row m, column n of
+  // the 32 x 32 tile sits in lane (m % 32) + 32 * ((n / 4) % 2), register
+  // (n % 4) + 4 * (n / 8): runs of 4 columns of one row per lane.
+  // The stages are free once every wave is past its last fragment read and
+  // its last (redundant) DMA has landed.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const int rl = lane & 31;
+  float sxr[FM];
+  int32_t zr[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    sxr[i] = lds_sx[wm * 128 + i * 32 + rl];
+    zr[i] = lds_z[wm * 128 + i * 32 + rl];
+  }
+  // The wave's 128 x 128 fp16 tile in LDS: row r (256 bytes) holds 16-byte
+  // chunk c at position c ^ (r & 15), and the two 8-byte halves of a chunk are
+  // swapped in rows with bit 4 set, so the 32 lanes of each half-wave's 8-byte
+  // writes (rows r .. r + 31) and the 16 lanes of each row's 16-byte reads
+  // cover all 64 banks.
+  uint8_t* const tile = smem + wave * (128 * 256);
+  const int half = ((lane >> 5) ^ (lane >> 4)) & 1;
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int cl = wn * 128 + j * 32 + 8 * q + 4 * (lane >> 5);
+      const float4 sw = *reinterpret_cast<const float4*>(lds_sw + cl);
+      const int4 sm = *reinterpret_cast<const int4*>(lds_sum + cl);
+      float4 bv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (BIAS) bv = *reinterpret_cast<const float4*>(lds_b + cl);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const v16i& a = acc[i][j];
+        float r0 = (float)(a[4 * q + 0] + __mul24(zr[i], sm.x)) * sxr[i];
+        float r1 = (float)(a[4 * q + 1] + __mul24(zr[i], sm.y)) * sxr[i];
+        float r2 = (float)(a[4 * q + 2] + __mul24(zr[i], sm.z)) * sxr[i];
+        float r3 = (float)(a[4 * q + 3] + __mul24(zr[i], sm.w)) * sxr[i];
+        r0 = r0 * sw.x;
+        r1 = r1 * sw.y;
+        r2 = r2 * sw.z;
+        r3 = r3 * sw.w;
+        if (BIAS) {
+          r0 = r0 + bv.x;
+          r1 = r1 + bv.y;
+          r2 = r2 + bv.z;
+          r3 = r3 + bv.w;
+        }
+        // The fp32 values are pinned before the narrowing, so no multiply or
+        // add is folded into it (one rounding of the fp32 result to fp16).
+        asm("" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3));
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        uint2 pk;
+        pk.x = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){r0, r1}, h2));
+        pk.y = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){r2, r3}, h2));
+        const int r = i * 32 + rl;
+        *reinterpret_cast<uint2*>(tile + r * 256 + 16 * ((4 * j + q) ^ (r & 15)) + 8 * half) = pk;
+      }
+    }
+  // A wave reads back only what its own lanes wrote.
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __half* const out = static_cast<__half*>(g.out);
+  const int c = lane & 15;
+  const int64_t col = n0 + wn * 128 + 8 * c;
+#pragma unroll
+  for (int sr = 0; sr < 32; ++sr) {
+    const int r = 4 * sr + (lane >> 4);
+    uint4 v = *reinterpret_cast<const uint4*>(tile + r * 256 + 16 * (c ^ (r & 15)));
+    if ((sr >> 2) & 1) {  // bit 4 of r: halves stored swapped
+      const uint32_t x = v.x, y = v.y;
+      v.x = v.z;
+      v.y = v.w;
+      v.z = x;
+      v.w = y;
+    }
+    const int64_t row = m0 + wm * 128 + r;
+    if (row < g.M && col < g.N) store_stream(v, out + row * g.N + col);
+  }
+}
+
+}  // namespace
+
+bool wide_gemm_fits(const GemmArgs& g) {
+  const int64_t KB = g.KP / 2;
+  return g.raw == nullptr && g.M >= 1 && g.N % 8 == 0 && KB % kSlice == 0 && KB > 0 &&
+         g.KP <= 65536 && (reinterpret_cast<uintptr_t>(g.out) & 15) == 0 &&
+         g.arows * KB <= 0xFFFFFFFFll && g.brows * KB <= 0xFFFFFFFFll;
+}
+
+int launch_wide_gemm(GemmArgs g, hipStream_t stream) {
+  if (!wide_gemm_fits(g)) return fail("internal: shape outside the wide-tile GEMM");
+  g.tiles_n = (int)((g.N + kTile - 1) / kTile);
+  const int64_t nblocks = ((g.M + kTile - 1) / kTile) * g.tiles_n;
+  if (nblocks > 0x7FFFFFFF) return fail("matmul: grid too large");
+  const dim3 grid((unsigned)nblocks), block(64 * kWaves);
+  if (g.bias)
+    launch(w4a4_gemm_wide_kernel<true>, grid, block, stream, g);
+  else
+    launch(w4a4_gemm_wide_kernel<false>, grid, block, stream, g);
+  return launch_status("w4a4_gemm_wide_kernel");
+}
+
+}  // namespace dscq

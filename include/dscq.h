@@ -270,6 +270,22 @@ int dscq_device_supported(void);
 int dscq_time_next_kernel(void* start, void* stop);
 
 /*
+ * GEMM kernel choice for this thread's later dscq_matmul / dscq_matmul_ws /
+ * dscq_matmul_noalloc calls (no reference counterpart; the analogue of the
+ * reference's force_decode for the dense kernels, for tests and measurement):
+ *   0  automatic (the default): the wide-tile kernel (256 x 256 tiles, one
+ *      wave per SIMD) for fp16 output without raw accumulators when its tiles
+ *      make at least two rounds of one tile per compute unit, else the
+ *      pipelined kernel;
+ *   1  the wide-tile kernel wherever it applies (fp16 output, no raw
+ *      accumulators, N % 8 == 0, K a multiple of 256, KP <= 65536, M >= 64);
+ *   2  never the wide-tile kernel.
+ * Every kernel gives the same results.  Returns the previous setting, or
+ * DSCQ_EINVAL for another value.
+ */
+int dscq_set_gemm_kernel(int which);
+
+/*
  * Measurement probes (no reference counterpart): the ceilings the kernels
  * above are compared against, timed on the same device in the same run (with
  * dscq_time_next_kernel like any other call).

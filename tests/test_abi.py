@@ -129,6 +129,19 @@ def test_c_other_argument_checks():
                                         d, d, d, None, None)
 
 
+def test_c_set_gemm_kernel_is_per_thread():
+    import threading
+    L = _lib.lib()
+    assert L.dscq_set_gemm_kernel(1) == 0
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(L.dscq_set_gemm_kernel(0)))
+    t.start()
+    t.join()
+    assert seen == [0]  # a new thread starts at automatic
+    assert L.dscq_set_gemm_kernel(0) == 1
+    assert "0, 1 or 2" in _einval("dscq_set_gemm_kernel", 5)
+
+
 def test_c_probe_argument_checks():
     d = 16
     assert "pieces" in _einval("dscq_stream_probe", d, 64, d, 16, 3, None)

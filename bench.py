@@ -81,9 +81,11 @@ def parse():
                    help="run the workload's steps back to back this long before timing anything "
                         "(from idle the GPU takes a few hundred milliseconds to reach its "
                         "steady clock)")
-    p.add_argument("--gemm-kernel", choices=("auto", "wide", "pipe"), default="auto",
+    p.add_argument("--gemm-kernel", choices=("auto", "wide", "pipe", "wide256", "wide128"),
+                   default="auto",
                    help="dense GEMM kernel (dscq_set_gemm_kernel): the automatic choice, the "
-                        "wide-tile kernel wherever it applies, or never the wide-tile kernel")
+                        "wide-tile kernel wherever it applies (with the automatic tile width, "
+                        "or 256 x 256 / 256 x 128 tiles), or never the wide-tile kernel")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-graph", action="store_true")
     p.add_argument("--kernels-only", action="store_true",
@@ -222,6 +224,10 @@ def probes(torch, dev):
 
 
 def kernel_class(name):
+    if "mfma_probe" in name:
+        return "mfma_probe"
+    if "stream_probe" in name:
+        return "stream_probe"
     if "row_quant" in name:
         # template arguments <T, ROT, MODE, ...>: MODE 1 is the weight pre-pack
         args = name.split("row_quant_kernel<", 1)[-1].split(",")
@@ -240,8 +246,13 @@ def gemm_kernel_name(M, N, K, choice, cus=256):
     outside the skinny-M range (the library's dispatch rule, restated)."""
     fits = N % 8 == 0 and K % 256 == 0 and K <= 65536 and M >= 64
     t256 = -(-M // 256) * -(-N // 256)
-    wide = fits and choice != "pipe" and (choice == "wide" or (M >= 256 and t256 >= 2 * cus))
-    return "w4a4_gemm_wide_kernel" if wide else "w4a4_gemm_pipe_kernel"
+    if not fits or choice == "pipe":
+        return "w4a4_gemm_pipe_kernel"
+    if choice in ("wide256", "wide128"):
+        return f"w4a4_gemm_wide_kernel<{choice[4:]}>"
+    if M >= 256 and t256 >= 2 * cus:
+        return "w4a4_gemm_wide_kernel<256>"
+    return "w4a4_gemm_wide_kernel<256>" if choice == "wide" else "w4a4_gemm_pipe_kernel"
 
 
 def traffic_summary(fetch_csv, write_csv):
@@ -302,7 +313,7 @@ def counter_summary(counter_csv, workload):
     acc, dur = {}, {}
     for row in csv.DictReader(open(counter_csv)):
         cls = kernel_class(row["Kernel_Name"])
-        if cls not in ("quantize", "gemm", "decode"):
+        if cls not in ("quantize", "gemm", "decode", "mfma_probe", "stream_probe"):
             continue
         acc.setdefault(cls, {}).setdefault(row["Counter_Name"], []).append(
             float(row["Counter_Value"]))
@@ -432,7 +443,8 @@ def main():
     import torch
     from dscquant_amd import _lib, w4a4
 
-    _lib.lib().dscq_set_gemm_kernel({"auto": 0, "wide": 1, "pipe": 2}[args.gemm_kernel])
+    _lib.lib().dscq_set_gemm_kernel(
+        {"auto": 0, "wide": 1, "pipe": 2, "wide256": 3, "wide128": 4}[args.gemm_kernel])
     if args.workload == "mlp":
         return main_mlp(args, torch, _lib, w4a4)
     if args.workload.startswith("decode"):

@@ -117,7 +117,7 @@ int dscq_time_next_kernel(void* start, void* stop) {
 }
 
 int dscq_set_gemm_kernel(int which) {
-  if (which < 0 || which > 2) return fail("set_gemm_kernel: 0, 1 or 2 (got %d)", which);
+  if (which < 0 || which > 4) return fail("set_gemm_kernel: 0 to 4 (got %d)", which);
   const int prev = g_gemm_kernel;
   g_gemm_kernel = which;
   return prev;

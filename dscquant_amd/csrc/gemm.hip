@@ -443,8 +443,9 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   gload(G1, 1);
   __builtin_amdgcn_sched_barrier(0);
   if (tid < BM) {
-    lds_sx[tid] = meta_sx;
-    lds_z[tid] = 8 - meta_z;
+    // Staged pre-scaled for the epilogue: sx / 256 and (8 - zx) * 256 (exact).
+    lds_sx[tid] = meta_sx * 0.00390625f;
+    lds_z[tid] = (8 - meta_z) * 256;
   }
   if (tid < BN) {
     lds_sw[tid] = meta_sw;
@@ -518,8 +519,11 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   // (m % 32) + 32 * ((n / 4) % 2), register (n % 4) + 4 * (n / 8).  Every lane
   // therefore holds runs of 4 consecutive columns of one row and writes them
   // straight to memory (8 bytes fp16 / 16 bytes fp32).  Operation order of
-  // kernel/w4a4.cu:74-77; |8 - zx| <= 8 and |sums| < 2^23, so the 24-bit
-  // multiply is exact.
+  // kernel/w4a4.cu:74-77, with the row factors staged as sx / 256 and
+  // (8 - zx) * 256: corrected * 256 = acc + (8 - zx) * 256 * sums is one
+  // v_mad_i32_i24 (|(8 - zx) * 256| <= 2048 and |sums| < 2^23 fit 24 bits; the
+  // sum stays below 2^31 for K <= 65536), and float(corrected * 256) * (sx / 256)
+  // equals float(corrected) * sx exactly (power-of-two scalings).
   // Row and column metadata were staged in LDS before the first barrier of
   // the K loop.
   const int rl = lane & 31;
@@ -560,8 +564,8 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
       if (BIAS) bc[j][q] = *reinterpret_cast<const float4*>(lds_b + cl);
     }
   auto value = [&](int i, int j, int v, float sw, int32_t sum, float b) {
-    const int32_t corrected = (acc[i][j][v] >> 8) + __mul24(zr[i], sum);
-    float res = (float)corrected * sxr[i];
+    const int32_t corrected256 = acc[i][j][v] + __mul24(zr[i], sum);
+    float res = (float)corrected256 * sxr[i];
     res = res * sw;
     if (BIAS) res = res + b;
     return res;
@@ -573,15 +577,14 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   // of 16-byte pieces of 32 rows (M=2048, N=4096: 2.1-2.6 us faster at every
   // K; the 16 MiB of output then take ~3.2 us).  Rows in LDS are 128 bytes, 16-byte
   // chunk c of row r stored at c ^ (r & 7), so 8 consecutive lanes -- 8 rows
-  // on the writes, one row on the reads -- cover all banks.  A wave reads back
-  // only what it wrote (its LDS accesses complete in order).
+  // on the writes, one row on the reads -- cover all banks.
   if constexpr (sizeof(OutT) == 2 && TN == 64) {
     static_assert(WM * WN * TM * TN * 2 <= 2 * STAGE, "staged tiles fit the slice buffers");
     if (!g.raw) {
       __syncthreads();
       uint8_t* const tile = smem + wave * (TM * TN * 2);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
+      // Rows i * 32 .. + 31 of the wave's tile into LDS.
+      auto stage_rows = [&](int i) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -589,18 +592,19 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
             const float4 sw = swc[j][q];
             const int4 sm = sumc[j][q];
             const float4 b = bc[j][q];
-            const __half h0 = to_out<__half>(value(i, j, 4 * q + 0, sw.x, sm.x, b.x));
-            const __half h1 = to_out<__half>(value(i, j, 4 * q + 1, sw.y, sm.y, b.y));
-            const __half h2 = to_out<__half>(value(i, j, 4 * q + 2, sw.z, sm.z, b.z));
-            const __half h3 = to_out<__half>(value(i, j, 4 * q + 3, sw.w, sm.w, b.w));
             uint2 pk;
-            pk.x = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
-            pk.y = (uint32_t)__half_as_ushort(h2) | ((uint32_t)__half_as_ushort(h3) << 16);
+            pk.x = pack_h2(value(i, j, 4 * q + 0, sw.x, sm.x, b.x),
+                           value(i, j, 4 * q + 1, sw.y, sm.y, b.y));
+            pk.y = pack_h2(value(i, j, 4 * q + 2, sw.z, sm.z, b.z),
+                           value(i, j, 4 * q + 3, sw.w, sm.w, b.w));
             const int lr = i * 32 + rl;
             *reinterpret_cast<uint2*>(tile + lr * 128 + 16 * ((4 * j + q) ^ (rl & 7)) +
                                       8 * (lane >> 5)) = pk;
           }
+      };
       if constexpr (GATED) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) stage_rows(i);
         // SiLU-gated MLP (weights interleaved in 64-row blocks: gate rows then
         // up rows of the same 64 outputs): the gate half of the tile's rows
         // is in the LDS tiles of waves (wm, 0), the up half in (wm, 1).  Wave
@@ -627,14 +631,23 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
         }
         return;
       }
+      // One 32-row group at a time: the group's stores go out while the next
+      // group is converted.  A wave reads back only what its own lanes wrote;
+      // the wave-scope fence orders their LDS writes before the reads.
       const int c8 = lane & 7;
       const int64_t col = n0 + wn * TN + 8 * c8;
 #pragma unroll
-      for (int s = 0; s < TM / 8; ++s) {
-        const int lr = 8 * s + (lane >> 3);
-        const uint4 v = *reinterpret_cast<const uint4*>(tile + lr * 128 + 16 * (c8 ^ (lr & 7)));
-        const int64_t row = m0 + wm * TM + lr;
-        if (row < g.M && col < g.N) store_stream(v, out + row * g.N + col);
+      for (int i = 0; i < FM; ++i) {
+        stage_rows(i);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int lr = i * 32 + 8 * s + (lane >> 3);
+          const uint4 v = *reinterpret_cast<const uint4*>(tile + lr * 128 + 16 * (c8 ^ (lr & 7)));
+          const int64_t row = m0 + wm * TM + lr;
+          if (row < g.M && col < g.N) store_stream(v, out + row * g.N + col);
+        }
       }
       return;
     }
@@ -656,11 +669,9 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
         const float r3 = value(i, j, 4 * q + 3, sw.w, sm.w, b.w);
         if (row < g.M && c0 < g.N) {
           if (sizeof(OutT) == 2) {
-            const __half h0 = to_out<__half>(r0), h1 = to_out<__half>(r1);
-            const __half h2 = to_out<__half>(r2), h3 = to_out<__half>(r3);
             uint2 pk;
-            pk.x = (uint32_t)__half_as_ushort(h0) | ((uint32_t)__half_as_ushort(h1) << 16);
-            pk.y = (uint32_t)__half_as_ushort(h2) | ((uint32_t)__half_as_ushort(h3) << 16);
+            pk.x = pack_h2(r0, r1);
+            pk.y = pack_h2(r2, r3);
             *reinterpret_cast<uint2*>(out + row * g.N + c0) = pk;
           } else {
             *reinterpret_cast<float4*>(out + row * g.N + c0) = make_float4(r0, r1, r2, r3);
@@ -1058,14 +1069,17 @@ bool use_pipe_mid_m(const GemmArgs& g, bool gated = false) {
 }
 
 // The wide-tile kernel (gemm_wide.hip) for fp16 output without raw
-// accumulators when its 256 x 256 tiles make at least two rounds of one tile
-// per CU (or wherever it applies, or never: dscq_set_gemm_kernel).
-bool use_wide(const GemmArgs& g, bool out_half) {
+// accumulators: its tile width (256 or 128), or 0 for another kernel.  256 x 256
+// tiles when they make at least two rounds of one tile per CU (or as
+// dscq_set_gemm_kernel forces).
+int use_wide(const GemmArgs& g, bool out_half) {
   const int pref = gemm_kernel_preference();
-  if (pref == 2 || !out_half || g.M < 64 || !wide_gemm_fits(g)) return false;
-  if (pref == 1) return true;
+  if (pref == 2 || !out_half || g.M < 64 || !wide_gemm_fits(g)) return 0;
+  if (pref == 3) return 256;
+  if (pref == 4) return 128;
   const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 255) / 256);
-  return g.M >= 256 && t256 >= 2 * cu_count();
+  if (g.M >= 256 && t256 >= 2 * cu_count()) return 256;
+  return pref == 1 ? 256 : 0;
 }
 
 template <typename OutT>
@@ -1090,7 +1104,7 @@ int gemm_typed(const GemmArgs& g, bool decode, int32_t* ws, int64_t ws_bytes,
   // 11.2 us).  Shorter rows keep the pipelined kernel (not measured there).
   // (The wide-tile kernel's own rule never meets the skinny one; checked
   // first so that a forced choice covers every M >= 64.)
-  if (use_wide(g, sizeof(OutT) == 2)) return launch_wide_gemm(g, stream);
+  if (const int bn = use_wide(g, sizeof(OutT) == 2)) return launch_wide_gemm(g, bn, stream);
   if (g.KP >= 4096 && g.KP <= 65536 && (g.M + 15) / 16 * g.N <= 16384)
     return launch_gemv<OutT>(g, stream);
   if (g.KP > 65536) return launch_cfg<OutT, 64, 64, 2, 2, true>(g, stream);

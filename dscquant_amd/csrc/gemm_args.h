@@ -29,14 +29,16 @@ struct GemmArgs {
   int tiles = 0;  // tiles per part
 };
 
-// The wide-tile kernel (gemm_wide.hip): 256 x 256 tiles, one wave per SIMD,
-// fp16 output without raw accumulators.  wide_gemm_fits says whether a shape
-// and its buffers meet the kernel's requirements; launch_wide_gemm runs it.
+// The wide-tile kernel (gemm_wide.hip): 256 x bn tiles (bn = 256 or 128),
+// one wave per SIMD, fp16 output without raw accumulators.  wide_gemm_fits
+// says whether a shape and its buffers meet the kernel's requirements;
+// launch_wide_gemm runs it.
 bool wide_gemm_fits(const GemmArgs& g);
-int launch_wide_gemm(GemmArgs g, hipStream_t stream);
+int launch_wide_gemm(GemmArgs g, int bn, hipStream_t stream);
 
 // This thread's GEMM kernel preference (dscq_set_gemm_kernel): 0 automatic,
-// 1 the wide-tile kernel wherever it applies, 2 never.
+// 1 the wide-tile kernel wherever it applies, 2 never, 3 / 4 the wide-tile
+// kernel with 256 x 256 / 256 x 128 tiles wherever it applies.
 int gemm_kernel_preference();
 
 }  // namespace dscq

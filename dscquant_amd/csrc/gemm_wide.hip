@@ -55,16 +55,14 @@
 namespace dscq {
 namespace {
 
-constexpr int kTile = 256;                    // rows of A and of B per tile
+constexpr int kTileM = 256;                   // rows of A per tile
 constexpr int kSlice = 128;                   // bytes of a packed row per slice
-constexpr int kHalf = kTile * kSlice;         // 32 KiB: one operand's rows of a slice
-constexpr int kStage = 2 * kHalf;             // 64 KiB per slice
-// LDS: A of stage 0, A of stage 1, B of stage 0, B of stage 1 (32 KiB each),
-// so that every fragment of either stage is within a ds_read immediate offset
+constexpr int kHalfA = kTileM * kSlice;       // 32 KiB: A's rows of one slice
+// LDS: A of stage 0, A of stage 1, then B of stage 0 and B of stage 1, so that
+// every fragment of either stage is within a ds_read immediate offset
 // (< 64 KiB) of one A base and one B base per unit.
-constexpr int kBRegion = 2 * kHalf;
+constexpr int kBRegion = 2 * kHalfA;
 constexpr int kWaves = 4;
-constexpr int kDma = 2 * kTile / 8 / kWaves;  // DMA instructions (8 rows each) per wave per slice
 
 __device__ __forceinline__ void barrier_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -85,15 +83,21 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
 }
 #pragma clang diagnostic pop
 
-template <bool BIAS>
+template <int BN, bool BIAS>
 __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs g) {
-  constexpr int FM = 4, FN = 4, NF = FM + FN;  // 128 x 128 per wave
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStage + kTile * 20];
-  float* const lds_sx = reinterpret_cast<float*>(smem + 2 * kStage);            // sx / 256
-  int32_t* const lds_z = reinterpret_cast<int32_t*>(smem + 2 * kStage + kTile * 4);  // (8 - zx) * 256
-  float* const lds_sw = reinterpret_cast<float*>(smem + 2 * kStage + kTile * 8);
-  int32_t* const lds_sum = reinterpret_cast<int32_t*>(smem + 2 * kStage + kTile * 12);
-  float* const lds_b = reinterpret_cast<float*>(smem + 2 * kStage + kTile * 16);
+  // 2 x 2 waves, each 128 x (BN / 2): 4 x FN MFMA tiles.
+  constexpr int FM = 4, FN = BN / 64, NF = FM + FN, TN = BN / 2, MF = FM * FN;
+  constexpr int kHalfB = BN * kSlice;           // B's rows of one slice
+  constexpr int kStages = kBRegion + 2 * kHalfB;
+  constexpr int kDma = (kTileM + BN) / 8 / kWaves;  // DMA instructions per wave per slice
+  static_assert(BN == 256 || BN == 128, "tile width");
+  static_assert(kDma % 2 == 0, "the per-lane DMA offset pairs with the parity of j");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kStages + kTileM * 8 + BN * 12];
+  float* const lds_sx = reinterpret_cast<float*>(smem + kStages);             // sx / 256
+  int32_t* const lds_z = reinterpret_cast<int32_t*>(smem + kStages + kTileM * 4);  // (8 - zx) * 256
+  float* const lds_sw = reinterpret_cast<float*>(smem + kStages + kTileM * 8);
+  int32_t* const lds_sum = reinterpret_cast<int32_t*>(smem + kStages + kTileM * 8 + BN * 4);
+  float* const lds_b = reinterpret_cast<float*>(smem + kStages + kTileM * 8 + BN * 8);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -101,38 +105,42 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   const int wm = wave >> 1, wn = wave & 1;
   const int tile_m = (int)(blockIdx.x / (unsigned)g.tiles_n);
   const int tile_n = (int)(blockIdx.x % (unsigned)g.tiles_n);
-  const int64_t m0 = (int64_t)tile_m * kTile, n0 = (int64_t)tile_n * kTile;
+  const int64_t m0 = (int64_t)tile_m * kTileM, n0 = (int64_t)tile_n * BN;
   const int64_t KB = g.KP / 2;
   const int nslices = (int)(KB / kSlice);
 
   // ---- DMA sources.  Instruction j of this wave covers the 8 tile rows
-  // 8d .. 8d + 7 (d = 16 wave + j) of A (waves 0-1) or B (waves 2-3); the
-  // tile origin and MP / NP are multiples of 8, so a group is wholly inside
-  // the operand's rows or wholly past them, and groups past them are clamped
-  // to its last 8 rows (their sums are never stored): a wave-uniform base per
-  // instruction.  Lane l reads row 8d + l / 8 at unit (l % 8) ^ ((row >> 1) & 7),
-  // and (row >> 1) & 7 = (4 (j % 2) + l / 16) % 8, so the per-lane offset
-  // depends on the parity of j only.
-  const bool a_side = wave < 2;
-  const uint8_t* const dbase = a_side ? g.a : g.b;
-  const int64_t rows_end = (a_side ? g.arows : g.brows) - 8;
-  const int64_t r0 = a_side ? m0 : n0 - kTile;  // operand row of tile row 0
-  const uint8_t* gbase[kDma];                    // wave-uniform: scalar registers
+  // 8d .. 8d + 7, d = kDma * wave + j, of the tile's 256 A rows followed by its
+  // BN B rows.  The tile origin and MP / NP are multiples of 8, so a group is
+  // wholly inside the operand's rows or wholly past them, and groups past them
+  // are clamped to its last 8 rows (their sums are never stored): a
+  // wave-uniform base per instruction.  Lane l reads row 8d + l / 8 at unit
+  // (l % 8) ^ ((row >> 1) & 7); (row >> 1) & 7 = (4 (d % 2) + l / 16) % 8 and
+  // kDma is even, so the per-lane offset depends on the parity of j only.
+  const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+      (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem);
+  const uint8_t* gbase[kDma];  // wave-uniform: scalar registers
+  uint32_t ldsj[kDma];         // LDS byte address of the group in stage 0
 #pragma unroll
-  for (int j = 0; j < kDma; ++j) gbase[j] = dbase + min(r0 + 8 * (kDma * wave + j), rows_end) * KB;
+  for (int j = 0; j < kDma; ++j) {
+    const int R = 8 * (kDma * wave + j);
+    if (R < kTileM) {
+      gbase[j] = g.a + min(m0 + R, g.arows - 8) * KB;
+      ldsj[j] = lds0 + (uint32_t)(R * kSlice);
+    } else {
+      gbase[j] = g.b + min(n0 + (R - kTileM), g.brows - 8) * KB;
+      ldsj[j] = lds0 + (uint32_t)(kBRegion + (R - kTileM) * kSlice);
+    }
+  }
   uint32_t lane_off[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p)
     lane_off[p] = (uint32_t)((lane >> 3) * KB + 16 * ((lane & 7) ^ ((4 * p + (lane >> 4)) & 7)));
-  // LDS destination of this wave's rows: its operand's region, rows
-  // (wave % 2) * 128 .. +127 of the tile.
-  const uint32_t lds_dma = (uint32_t)__builtin_amdgcn_readfirstlane(
-      (int)((uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem +
-            (uint32_t)((a_side ? 0 : kBRegion) + (wave & 1) * 128 * kSlice)));
-  // Instruction j of slice `slice` into `stage`; the slice offset rides on the
+  // Instruction j of a slice into `stage`: the slice offset rides on the
   // per-lane offsets (off[p] = lane_off[p] + slice * 128), the bases stay put.
   auto dma_one = [&](int j, const uint32_t (&off)[2], int stage) {
-    dma16(gbase[j], off[j & 1], lds_dma + (uint32_t)(stage * kHalf + j * 8 * kSlice));
+    const int R = 8 * (kDma * wave + j);
+    dma16(gbase[j], off[j & 1], ldsj[j] + (uint32_t)stage * (R < kTileM ? kHalfA : kHalfB));
   };
   auto dma = [&](int slice, int stage) {
     const uint32_t off[2] = {lane_off[0] + (uint32_t)slice * kSlice,
@@ -150,21 +158,21 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   for (int q = 0; q < 4; ++q) {
     const uint32_t qo = 16 * ((2 * q + (lane >> 5)) ^ fsw);
     abase[q] = (uint32_t)((wm * 128 + fr) * kSlice) + qo;
-    bbase[q] = (uint32_t)(kBRegion + (wn * 128 + fr) * kSlice) + qo;
+    bbase[q] = (uint32_t)(kBRegion + (wn * TN + fr) * kSlice) + qo;
   }
   uint4 P[4][NF];
   auto lread = [&](int stage, int q) {
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      const uint32_t off = f < FM ? abase[q] + (uint32_t)(stage * kHalf + f * 32 * kSlice)
-                                  : bbase[q] + (uint32_t)(stage * kHalf + (f - FM) * 32 * kSlice);
+      const uint32_t off = f < FM ? abase[q] + (uint32_t)(stage * kHalfA + f * 32 * kSlice)
+                                  : bbase[q] + (uint32_t)(stage * kHalfB + (f - FM) * 32 * kSlice);
       P[q][f] = *reinterpret_cast<const uint4*>(smem + off);
     }
   };
 
   // Accumulators: the first MFMA of each takes a literal zero as its C operand
   // (slice 0's first step, peeled), so no registers are ever zero-filled --
-  // a zero-filled accumulator array is 256 VGPRs that only then move to AGPRs.
+  // a zero-filled accumulator array takes VGPRs that only then move to AGPRs.
   v16i acc[FM][FN];
   v4i U0[NF], U1[NF];
   // k-step t of a slice uses P[t / 2] dwords (2 * (t % 2), +1).
@@ -197,12 +205,13 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
     U[f][2 * h] = (int)((x << 4) & 0xF0F0F0F0u);
     U[f][2 * h + 1] = (int)(x & 0xF0F0F0F0u);
   };
-  // One MFMA, then three of the step's unpack VALU instructions, and so on.
+  // One MFMA, then a share of the step's unpack VALU instructions, and so on.
+  constexpr int VPM = (6 * NF + MF - 1) / MF;
   auto interleave = [&]() {
 #pragma unroll
-    for (int k = 0; k < FM * FN; ++k) {
+    for (int k = 0; k < MF; ++k) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -219,9 +228,11 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // slice 0 and the metadata
   lds_sx[tid] = meta_sx * 0.00390625f;                // exact: a power-of-two scaling
   lds_z[tid] = (8 - meta_z) * 256;
-  lds_sw[tid] = meta_sw;
-  lds_sum[tid] = meta_sum;
-  if (BIAS) lds_b[tid] = meta_b;
+  if (tid < BN) {
+    lds_sw[tid] = meta_sw;
+    lds_sum[tid] = meta_sum;
+    if (BIAS) lds_b[tid] = meta_b;
+  }
   if (nslices > 1) dma(1, 1);
   barrier_lds();
   lread(0, 0);
@@ -230,8 +241,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
 
   // The barrier and the reads of the next slice's first units run after the
   // last slice too (they read a stage nothing uses any more, and the unpack
-  // result is dropped), so one body serves every slice; only the DMA of slice
-  // s + 2 depends on whether it exists (a uniform branch between two steps).
+  // result is dropped), so one body serves every slice.
   auto slice = [&](int s, auto stage, auto first) {
     constexpr int C = decltype(stage)::value, NX = C ^ 1;
     if constexpr (decltype(first)::value)
@@ -257,10 +267,10 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of slice s + 1
     barrier_lds();
     lread(NX, 0);
-    // Step 5 by hand: sixteen groups of one MFMA, three unpack instructions
-    // of step 6 and one DMA instruction, so the loads issue in the MFMAs'
-    // shadow instead of in a burst before them.  The DMA is unconditional
-    // (no branch around MFMA code, whose accumulators would be copied at the
+    // Step 5 by hand: MF groups of one MFMA, a share of the unpack of step 6
+    // and a share of the DMA of slice s + 2, so the loads issue in the MFMAs'
+    // shadow instead of in a burst before them.  The DMA is unconditional (no
+    // branch around MFMA code, whose accumulators would be copied at the
     // join): in the last two slices it reloads the last slice into stage c,
     // whose reads all completed before the barrier above; the epilogue waits
     // for it before it reuses the stages.
@@ -268,11 +278,14 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
       const uint32_t sl = (uint32_t)min(s + 2, nslices - 1) * kSlice;
       const uint32_t off[2] = {lane_off[0] + sl, lane_off[1] + sl};
 #pragma unroll
-      for (int k = 0; k < FM * FN; ++k) {
-        const int i = k / FN, j = k % FN;
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(U1[FM + j], U1[i], acc[i][j], 0, 0, 0);
-        unpack_half(U0, 6, k / 2, k % 2);
-        dma_one(k, off, C);
+      for (int k = 0; k < MF; ++k) {
+        acc[k / FN][k % FN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+            U1[FM + k % FN], U1[k / FN], acc[k / FN][k % FN], 0, 0, 0);
+#pragma unroll
+        for (int pc = k * 2 * NF / MF; pc < (k + 1) * 2 * NF / MF; ++pc)
+          unpack_half(U0, 6, pc / 2, pc % 2);
+#pragma unroll
+        for (int j = k * kDma / MF; j < (k + 1) * kDma / MF; ++j) dma_one(j, off, C);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -307,18 +320,19 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
     sxr[i] = lds_sx[wm * 128 + i * 32 + rl];
     zr[i] = lds_z[wm * 128 + i * 32 + rl];
   }
-  // The wave's 128 x 128 fp16 tile in LDS: row r (256 bytes) holds 16-byte
-  // chunk c at position c ^ (r & 15), and the two 8-byte halves of a chunk are
-  // swapped in rows with bit 4 set, so the 32 lanes of each half-wave's 8-byte
-  // writes (rows r .. r + 31) and the 16 lanes of each row's 16-byte reads
-  // cover all 64 banks.
-  uint8_t* const tile = smem + wave * (128 * 256);
-  const int half = ((lane >> 5) ^ (lane >> 4)) & 1;
+  // The wave's 128 x TN fp16 tile in LDS: row r (RB = 2 TN bytes, CPR 16-byte
+  // chunks) holds chunk c at position c ^ (r % CPR), the two 8-byte halves of a
+  // chunk swapped in rows with bit log2(CPR) set, so that a half-wave's 8-byte
+  // writes (rows r .. r + 31) spread over the banks and every row's 16-byte
+  // reads cover them.
+  constexpr int RB = 2 * TN, CPR = TN / 8, LCPR = CPR == 16 ? 4 : 3, RPI = 64 / CPR;
+  uint8_t* const tile = smem + wave * (128 * RB);
+  const int half = ((lane >> 5) ^ (rl >> LCPR)) & 1;
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int cl = wn * 128 + j * 32 + 8 * q + 4 * (lane >> 5);
+      const int cl = wn * TN + j * 32 + 8 * q + 4 * (lane >> 5);
       const float4 sw = *reinterpret_cast<const float4*>(lds_sw + cl);
       const int4 sm = *reinterpret_cast<const int4*>(lds_sum + cl);
       float4 bv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -340,29 +354,25 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
           r2 = r2 + bv.z;
           r3 = r3 + bv.w;
         }
-        // The fp32 values are pinned before the narrowing, so no multiply or
-        // add is folded into it (one rounding of the fp32 result to fp16).
-        asm("" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3));
-        typedef float f2 __attribute__((ext_vector_type(2)));
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         uint2 pk;
-        pk.x = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){r0, r1}, h2));
-        pk.y = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){r2, r3}, h2));
+        pk.x = pack_h2(r0, r1);
+        pk.y = pack_h2(r2, r3);
         const int r = i * 32 + rl;
-        *reinterpret_cast<uint2*>(tile + r * 256 + 16 * ((4 * j + q) ^ (r & 15)) + 8 * half) = pk;
+        *reinterpret_cast<uint2*>(tile + r * RB + 16 * ((4 * j + q) ^ (r & (CPR - 1))) +
+                                  8 * half) = pk;
       }
     }
   // A wave reads back only what its own lanes wrote.
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __half* const out = static_cast<__half*>(g.out);
-  const int c = lane & 15;
-  const int64_t col = n0 + wn * 128 + 8 * c;
+  const int c = lane % CPR;
+  const int64_t col = n0 + wn * TN + 8 * c;
 #pragma unroll
-  for (int sr = 0; sr < 32; ++sr) {
-    const int r = 4 * sr + (lane >> 4);
-    uint4 v = *reinterpret_cast<const uint4*>(tile + r * 256 + 16 * (c ^ (r & 15)));
-    if ((sr >> 2) & 1) {  // bit 4 of r: halves stored swapped
+  for (int sr = 0; sr < 128 / RPI; ++sr) {
+    const int r = RPI * sr + lane / CPR;
+    uint4 v = *reinterpret_cast<const uint4*>(tile + r * RB + 16 * (c ^ (r & (CPR - 1))));
+    if ((sr >> (2 * LCPR - 6)) & 1) {  // bit log2(CPR) of r: halves stored swapped
       const uint32_t x = v.x, y = v.y;
       v.x = v.z;
       v.y = v.w;
@@ -383,16 +393,24 @@ bool wide_gemm_fits(const GemmArgs& g) {
          g.arows * KB <= 0xFFFFFFFFll && g.brows * KB <= 0xFFFFFFFFll;
 }
 
-int launch_wide_gemm(GemmArgs g, hipStream_t stream) {
-  if (!wide_gemm_fits(g)) return fail("internal: shape outside the wide-tile GEMM");
-  g.tiles_n = (int)((g.N + kTile - 1) / kTile);
-  const int64_t nblocks = ((g.M + kTile - 1) / kTile) * g.tiles_n;
+int launch_wide_gemm(GemmArgs g, int bn, hipStream_t stream) {
+  if (!wide_gemm_fits(g) || (bn != 256 && bn != 128))
+    return fail("internal: shape outside the wide-tile GEMM");
+  g.tiles_n = (int)((g.N + bn - 1) / bn);
+  const int64_t nblocks = ((g.M + kTileM - 1) / kTileM) * g.tiles_n;
   if (nblocks > 0x7FFFFFFF) return fail("matmul: grid too large");
   const dim3 grid((unsigned)nblocks), block(64 * kWaves);
-  if (g.bias)
-    launch(w4a4_gemm_wide_kernel<true>, grid, block, stream, g);
-  else
-    launch(w4a4_gemm_wide_kernel<false>, grid, block, stream, g);
+#define DSCQ_WIDE(BNV)                                                   \
+  if (g.bias)                                                            \
+    launch(w4a4_gemm_wide_kernel<BNV, true>, grid, block, stream, g);    \
+  else                                                                   \
+    launch(w4a4_gemm_wide_kernel<BNV, false>, grid, block, stream, g);
+  if (bn == 256) {
+    DSCQ_WIDE(256)
+  } else {
+    DSCQ_WIDE(128)
+  }
+#undef DSCQ_WIDE
   return launch_status("w4a4_gemm_wide_kernel");
 }
 

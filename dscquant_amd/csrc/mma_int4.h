@@ -42,4 +42,15 @@ __device__ __forceinline__ float to_out<float>(float v) {
   return v;
 }
 
+// Two fp32 results narrowed to fp16 (round to nearest even) and packed, low
+// half first: one v_cvt_pk_f16_f32.  The values are pinned first, so no
+// preceding multiply or add is folded into the narrowing (one rounding of the
+// fp32 result, as to_out<__half>).
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  asm("" : "+v"(lo), "+v"(hi));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, h2));
+}
+
 }  // namespace dscq

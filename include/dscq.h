@@ -278,8 +278,11 @@ int dscq_time_next_kernel(void* start, void* stop);
  *      make at least two rounds of one tile per compute unit, else the
  *      pipelined kernel;
  *   1  the wide-tile kernel wherever it applies (fp16 output, no raw
- *      accumulators, N % 8 == 0, K a multiple of 256, KP <= 65536, M >= 64);
- *   2  never the wide-tile kernel.
+ *      accumulators, N % 8 == 0, K a multiple of 256, KP <= 65536, M >= 64),
+ *      with the tile width the automatic rule would take (256 by default);
+ *   2  never the wide-tile kernel;
+ *   3, 4  the wide-tile kernel wherever it applies, with 256 x 256 / 256 x 128
+ *      tiles.
  * Every kernel gives the same results.  Returns the previous setting, or
  * DSCQ_EINVAL for another value.
  */

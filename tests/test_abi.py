@@ -139,7 +139,7 @@ def test_c_set_gemm_kernel_is_per_thread():
     t.join()
     assert seen == [0]  # a new thread starts at automatic
     assert L.dscq_set_gemm_kernel(0) == 1
-    assert "0, 1 or 2" in _einval("dscq_set_gemm_kernel", 5)
+    assert "0 to 4" in _einval("dscq_set_gemm_kernel", 5)
 
 
 def test_c_probe_argument_checks():

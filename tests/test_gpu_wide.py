@@ -1,6 +1,6 @@
-"""GPU parity of the wide-tile GEMM kernel (256 x 256 tiles, one wave per SIMD,
-LDS-DMA operand loads; dscq_set_gemm_kernel selects it for any shape it
-applies to).
+"""GPU parity of the wide-tile GEMM kernel (256 x 256 and 256 x 128 tiles, one
+wave per SIMD, LDS-DMA operand loads; dscq_set_gemm_kernel selects it, and
+its tile width, for any shape it applies to).
 
 Its fp16 outputs are compared bit for bit with the oracle's epilogue on the
 oracle's int32 accumulators (kernel/w4a4.cu:70-161) at ragged shapes (partial
@@ -46,15 +46,16 @@ WIDE_CASES = [
 ]
 
 
+@pytest.mark.parametrize("width", [256, 128])
 @pytest.mark.parametrize("M,N,K,use_bias", WIDE_CASES,
                          ids=[f"M{c[0]}-N{c[1]}-K{c[2]}-bias{int(c[3])}" for c in WIDE_CASES])
-def test_wide_kernel_matches_oracle(gpu, M, N, K, use_bias):
-    print(f"wide case M{M} N{N} K{K} bias{use_bias}", flush=True)
+def test_wide_kernel_matches_oracle(gpu, M, N, K, use_bias, width):
+    print(f"wide case M{M} N{N} K{K} bias{use_bias} width{width}", flush=True)
     a, b, sx, zx, sw, sums = _operands(M, N, K, seed=11 * M + N + 3 * K)
     bias = np.random.default_rng(K + 1).standard_normal(N).astype(np.float16) if use_bias else None
     T = lambda v: torch.from_numpy(v).to(gpu)  # noqa: E731
     tbias = T(bias) if use_bias else torch.empty(0, dtype=torch.float16, device=gpu)
-    with gemm_kernel(1):
+    with gemm_kernel(3 if width == 256 else 4):
         out, raw = w4a4.matmul(T(a), T(b), T(sx), T(zx), T(sw), T(sums), tbias, M, N,
                                fused=True)
     with gemm_kernel(2):
@@ -73,8 +74,9 @@ def test_wide_kernel_matches_oracle(gpu, M, N, K, use_bias):
     assert rel[big].max() <= 1e-3
 
 
+@pytest.mark.parametrize("width", [256, 128])
 @pytest.mark.parametrize("zero_point", [0, 8, 15])
-def test_wide_kernel_extreme_magnitudes(gpu, zero_point):
+def test_wide_kernel_extreme_magnitudes(gpu, zero_point, width):
     """K = 65536 (the kernel's limit) with all -8 x -8 and -8 x +7 products: the
     largest scaled accumulators (2^30), and zero-points 0 / 15 with the largest
     code sums (the (8 - zx) * 256 * sums term at 2^29.8)."""
@@ -88,7 +90,7 @@ def test_wide_kernel_extreme_magnitudes(gpu, zero_point):
     sw = np.full(N, 2.0 ** -10, np.float32)
     sums = np.where(np.arange(N) < N // 2, -7 * K, 7 * K).astype(np.int32)
     T = lambda v: torch.from_numpy(v).to(gpu)  # noqa: E731
-    with gemm_kernel(1):
+    with gemm_kernel(3 if width == 256 else 4):
         out, _ = w4a4.matmul(T(a), T(b), T(sx), T(zx), T(sw), T(sums),
                              torch.empty(0, dtype=torch.float16, device=gpu), M, N, fused=True)
     torch.cuda.synchronize()
@@ -132,5 +134,5 @@ def test_set_gemm_kernel_contract(gpu):
     prev = L.dscq_set_gemm_kernel(1)
     assert L.dscq_set_gemm_kernel(2) == 1
     assert L.dscq_set_gemm_kernel(0) == 2
-    assert L.dscq_set_gemm_kernel(3) == -1
+    assert L.dscq_set_gemm_kernel(5) == -1
     L.dscq_set_gemm_kernel(prev)

@@ -245,12 +245,13 @@ def gemm_kernel_name(M, N, K, choice, cus=256):
     """The dense kernel dscq_matmul takes for an fp16 M x N x K GEMM at M >= 64
     outside the skinny-M range (the library's dispatch rule, restated)."""
     fits = N % 8 == 0 and K % 256 == 0 and K <= 65536 and M >= 64
-    t256 = -(-M // 256) * -(-N // 256)
+    rows = -(-M // 256)
+    t256, t128 = rows * -(-N // 256), rows * -(-N // 128)
     if not fits or choice == "pipe":
         return "w4a4_gemm_pipe_kernel"
     if choice in ("wide256", "wide128"):
         return f"w4a4_gemm_wide_kernel<{choice[4:]}>"
-    if M >= 256 and t256 >= 2 * cus:
+    if M >= 256 and 4 * t256 >= 3 * cus and 18 * -(-t256 // cus) <= 10 * -(-t128 // cus):
         return "w4a4_gemm_wide_kernel<256>"
     return "w4a4_gemm_wide_kernel<256>" if choice == "wide" else "w4a4_gemm_pipe_kernel"
 

@@ -1069,16 +1069,25 @@ bool use_pipe_mid_m(const GemmArgs& g, bool gated = false) {
 }
 
 // The wide-tile kernel (gemm_wide.hip) for fp16 output without raw
-// accumulators: its tile width (256 or 128), or 0 for another kernel.  256 x 256
-// tiles when they make at least two rounds of one tile per CU (or as
-// dscq_set_gemm_kernel forces).
+// accumulators: its tile width (256 or 128), or 0 for another kernel.
+// 256 x 256 tiles (or as dscq_set_gemm_kernel forces) when they fill at least
+// three quarters of a round of one tile per CU and their rounds, each worth 1.8
+// rounds of the pipelined kernel's 256 x 128 tiles (the wide kernel does the
+// same work ~10% faster), take no longer.  Measured in steps, pipelined /
+// wide: 4096 x 4096 x 4096 (256 tiles) 56.4 / 54.6 us; 3584 x 4096 x 4096 (224)
+// 51.9 / 48.9; 4096 x 11008 x 4096 (688) 168.8 / 149.6; 1024 x 16384 x 8192
+// 104.5 / 92.5; 3072 x 8192 x 8192 (384: three full pipelined rounds) 155.5 /
+// 166.6; 2048 x 4096 x 4096 (128) 28.7 / 43.4.
 int use_wide(const GemmArgs& g, bool out_half) {
   const int pref = gemm_kernel_preference();
   if (pref == 2 || !out_half || g.M < 64 || !wide_gemm_fits(g)) return 0;
   if (pref == 3) return 256;
   if (pref == 4) return 128;
-  const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 255) / 256);
-  if (g.M >= 256 && t256 >= 2 * cu_count()) return 256;
+  const int64_t cus = cu_count();
+  const int64_t rows = (g.M + 255) / 256;
+  const int64_t t256 = rows * ((g.N + 255) / 256), t128 = rows * ((g.N + 127) / 128);
+  const int64_t wide_rounds = (t256 + cus - 1) / cus, pipe_rounds = (t128 + cus - 1) / cus;
+  if (g.M >= 256 && 4 * t256 >= 3 * cus && 18 * wide_rounds <= 10 * pipe_rounds) return 256;
   return pref == 1 ? 256 : 0;
 }
 

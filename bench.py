@@ -282,7 +282,8 @@ def traffic_summary(fetch_csv, write_csv):
         if cls in means:
             fb = means[cls]["FETCH_SIZE"] * f_fetch
             wb = means[cls]["WRITE_SIZE"] * f_write
-            out[cls] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "traffic": round(fb + wb)}
+            out[cls] = {"fetch_bytes": round(fb), "write_bytes": round(wb),
+                        "traffic": round(fb) + round(wb)}
     return out
 
 

@@ -1,27 +1,30 @@
-// Wide-tile W4A4 GEMM for gfx950: 256 x 256 output tiles, one workgroup of
-// four waves per CU (one wave per SIMD), each wave a 128 x 128 block of 4 x 4
-// v_mfma_i32_32x32x32_i8 tiles whose 256 accumulator registers live in AGPRs.
+// Wide-tile W4A4 GEMM for gfx950: 256 x BN output tiles (BN = 256, or 128),
+// one workgroup of four waves per CU (one wave per SIMD), 2 x 2 waves each a
+// 128 x BN/2 block of 4 x BN/64 v_mfma_i32_32x32x32_i8 tiles whose
+// accumulators (256 or 128 registers) live in AGPRs.
 //
 // Semantics as gemm.hip (kernel/w4a4.cu:70-161): both operands are packed
 // int4, K-contiguous; nibbles are unpacked to int8 (x16) in registers
 // (mma_int4.h), so the int32 sums carry a factor 256.
 //
-// Data moved per multiply-accumulate, against the pipelined kernel's 256 x 128
-// tile of eight 64 x 64 waves: per MFMA a wave reads half a 16-byte fragment
-// from LDS (8 fragments feed 16 MFMAs per k-step) instead of one, and spends 3
-// VALU instructions on unpacking instead of 6; the tile loads (256 + 256) rows
-// per 65536 outputs instead of (256 + 128) per 32768, a third fewer bytes.
+// Data moved per multiply-accumulate at BN = 256, against the pipelined
+// kernel's 256 x 128 tile of eight 64 x 64 waves: per MFMA a wave reads half a
+// 16-byte fragment from LDS (8 fragments feed 16 MFMAs per k-step) instead of
+// one, and spends 3 VALU instructions on unpacking instead of 6; the tile loads
+// (256 + 256) rows per 65536 outputs instead of (256 + 128) per 32768, a third
+// fewer bytes.  BN = 128: 6 fragments per 8 MFMAs, 4.5 unpack instructions.
 //
 // K advances in 256-nibble slices: 128 bytes of every A and B row of the tile,
-// 64 KiB per slice, double-buffered in LDS.  Global memory reaches LDS by DMA
-// (global_load_lds_dwordx4, 16 bytes per lane written straight to LDS, no
-// register staging): instruction j of wave w fills 8 rows, 8d .. 8d + 7 of the
-// tile's 512 (d = 16 w + j: A rows 0-255 from waves 0-1, B rows from waves
-// 2-3); lane l writes position l % 8 of row 8d + l / 8, so it loads the row's
+// 32 KiB + BN * 128 bytes per slice, double-buffered in LDS.  Global memory
+// reaches LDS by DMA (global_load_lds_dwordx4, 16 bytes per lane written
+// straight to LDS, no register staging): each wave issues (256 + BN) / 32 such
+// instructions per slice; instruction j of wave w fills 8 rows, 8d .. 8d + 7 of
+// the tile's 256 + BN (d = (256 + BN) / 32 * w + j: A rows first, then B
+// rows); lane l writes position l % 8 of row 8d + l / 8, so it loads the row's
 // 16-byte unit (l % 8) ^ ((row >> 1) & 7): the pipelined kernel's swizzle,
 // applied on the global side, which keeps the fragment reads conflict-free.
 //
-// Schedule of slice s (LDS stage c = s & 1), k-steps 0..7 of 16 MFMAs each;
+// Schedule of slice s (LDS stage c = s & 1), k-steps 0..7 of 4 * BN / 64 MFMAs;
 // every step interleaves its MFMAs with the unpack of the next step:
 //   steps 1, 3   fragment units q = 2, 3 of slice s read from stage c
 //   before 5     this wave's DMA of slice s + 1 waited for (vmcnt), then a
@@ -42,8 +45,8 @@
 // float(corrected) * sx exactly (power-of-two scalings, no overflow: |acc| <=
 // 2^30 and |corrected| < 2^23 for K <= 65536); then * sw (+ bias) and one fp16
 // rounding (v_cvt_pk_f16_f32), the reference's operation order.  Each wave's
-// 128 x 128 fp16 tile goes through LDS (the idle slice stages) so that every
-// store instruction writes four whole 256-byte row segments.
+// 128 x BN/2 fp16 tile goes through LDS (the idle slice stages) so that every
+// store instruction writes whole row segments (four of 256 bytes at BN = 256).
 
 #include <type_traits>
 

@@ -77,6 +77,7 @@ def test_traffic_summary_scales_by_the_copy(tmp_path):
     ("prefill", ("quantize", "gemm")),
     ("decode1", ("decode",)),
     ("decode16", ("quantize", "gemm")),
+    ("70b_qo", ("quantize", "gemm")),
 ])
 def test_committed_traffic_blocks(workload, classes):
     """The blocks bench.py reads for roofline.traffic parse and are self-consistent."""
@@ -87,8 +88,8 @@ def test_committed_traffic_blocks(workload, classes):
     assert abs(cal["fetch_factor"] - cal["copy_bytes_each_way"] / cal["fetch_counter_bytes"]) < 1e-3
     for c in classes:
         assert t[c]["traffic"] == t[c]["fetch_bytes"] + t[c]["write_bytes"]
-    if workload == "prefill":
-        M, N, K, _ = bench.WORKLOADS["prefill"]
+    if workload in ("prefill", "70b_qo"):
+        M, N, K, _ = bench.WORKLOADS[workload]
         # the GEMM writes exactly its fp16 output; the quantize kernel its packed codes and
         # metadata, where each row's 4-byte scale and zero-point may take a 32-byte granule
         assert abs(t["gemm"]["write_bytes"] - 2 * M * N) < 16 * 1024  # counter noise: ~1 KiB

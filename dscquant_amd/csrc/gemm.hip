@@ -564,7 +564,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
       if (BIAS) bc[j][q] = *reinterpret_cast<const float4*>(lds_b + cl);
     }
   auto value = [&](int i, int j, int v, float sw, int32_t sum, float b) {
-    const int32_t corrected256 = acc[i][j][v] + __mul24(zr[i], sum);
+    const int32_t corrected256 = mad_i24(zr[i], sum, acc[i][j][v]);
     float res = (float)corrected256 * sxr[i];
     res = res * sw;
     if (BIAS) res = res + b;
@@ -636,17 +636,36 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
       // the wave-scope fence orders their LDS writes before the reads.
       const int c8 = lane & 7;
       const int64_t col = n0 + wn * TN + 8 * c8;
+      // A tile inside the output (every tile of a grid whose M and N are
+      // multiples of the tile) stores without per-row tests: a wave-uniform
+      // row base plus a 32-bit lane offset, all of a group's LDS reads issued
+      // before its stores.
+      const int wv = __builtin_amdgcn_readfirstlane(wave);
+      const bool whole = m0 + BM <= g.M && n0 + BN <= g.N;
+      const uint8_t* const obase = reinterpret_cast<const uint8_t*>(out) +
+                                   2 * ((m0 + (wv / WN) * TM) * g.N + n0 + (wv % WN) * TN);
+      const uint32_t lane_off = (uint32_t)(2 * ((lane >> 3) * g.N + 8 * c8));
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         stage_rows(i);
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         __builtin_amdgcn_wave_barrier();
+        uint4 v[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const int lr = i * 32 + 8 * s + (lane >> 3);
-          const uint4 v = *reinterpret_cast<const uint4*>(tile + lr * 128 + 16 * (c8 ^ (lr & 7)));
-          const int64_t row = m0 + wm * TM + lr;
-          if (row < g.M && col < g.N) store_stream(v, out + row * g.N + col);
+          v[s] = *reinterpret_cast<const uint4*>(tile + lr * 128 + 16 * (c8 ^ (lr & 7)));
+        }
+        if (whole) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            store_stream(v[s], const_cast<uint8_t*>(obase) + 2 * (i * 32 + 8 * s) * g.N + lane_off);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int64_t row = m0 + wm * TM + i * 32 + 8 * s + (lane >> 3);
+            if (row < g.M && col < g.N) store_stream(v[s], out + row * g.N + col);
+          }
         }
       }
       return;

@@ -343,10 +343,10 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const v16i& a = acc[i][j];
-        float r0 = (float)(a[4 * q + 0] + __mul24(zr[i], sm.x)) * sxr[i];
-        float r1 = (float)(a[4 * q + 1] + __mul24(zr[i], sm.y)) * sxr[i];
-        float r2 = (float)(a[4 * q + 2] + __mul24(zr[i], sm.z)) * sxr[i];
-        float r3 = (float)(a[4 * q + 3] + __mul24(zr[i], sm.w)) * sxr[i];
+        float r0 = (float)mad_i24(zr[i], sm.x, a[4 * q + 0]) * sxr[i];
+        float r1 = (float)mad_i24(zr[i], sm.y, a[4 * q + 1]) * sxr[i];
+        float r2 = (float)mad_i24(zr[i], sm.z, a[4 * q + 2]) * sxr[i];
+        float r3 = (float)mad_i24(zr[i], sm.w, a[4 * q + 3]) * sxr[i];
         r0 = r0 * sw.x;
         r1 = r1 * sw.y;
         r2 = r2 * sw.z;
@@ -371,19 +371,41 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   __half* const out = static_cast<__half*>(g.out);
   const int c = lane % CPR;
   const int64_t col = n0 + wn * TN + 8 * c;
+  // A tile inside the output stores without per-row tests: a wave-uniform row
+  // base plus a 32-bit lane offset, the LDS reads of eight store instructions
+  // issued before their stores.
+  const bool whole = m0 + kTileM <= g.M && n0 + BN <= g.N;
+  uint8_t* const obase =
+      reinterpret_cast<uint8_t*>(out) + 2 * ((m0 + wm * 128) * g.N + n0 + wn * TN);
+  const uint32_t out_off = (uint32_t)(2 * ((lane / CPR) * g.N + 8 * c));
+  constexpr int kBatch = 8;
 #pragma unroll
-  for (int sr = 0; sr < 128 / RPI; ++sr) {
-    const int r = RPI * sr + lane / CPR;
-    uint4 v = *reinterpret_cast<const uint4*>(tile + r * RB + 16 * (c ^ (r & (CPR - 1))));
-    if ((sr >> (2 * LCPR - 6)) & 1) {  // bit log2(CPR) of r: halves stored swapped
-      const uint32_t x = v.x, y = v.y;
-      v.x = v.z;
-      v.y = v.w;
-      v.z = x;
-      v.w = y;
+  for (int sb = 0; sb < 128 / RPI; sb += kBatch) {
+    uint4 v[kBatch];
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t) {
+      const int sr = sb + t;
+      const int r = RPI * sr + lane / CPR;
+      v[t] = *reinterpret_cast<const uint4*>(tile + r * RB + 16 * (c ^ (r & (CPR - 1))));
+      if ((sr >> (2 * LCPR - 6)) & 1) {  // bit log2(CPR) of r: halves stored swapped
+        const uint32_t x = v[t].x, y = v[t].y;
+        v[t].x = v[t].z;
+        v[t].y = v[t].w;
+        v[t].z = x;
+        v[t].w = y;
+      }
     }
-    const int64_t row = m0 + wm * 128 + r;
-    if (row < g.M && col < g.N) store_stream(v, out + row * g.N + col);
+    if (whole) {
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t)
+        store_stream(v[t], obase + 2 * (int64_t)(RPI * (sb + t)) * g.N + out_off);
+    } else {
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        const int64_t row = m0 + wm * 128 + RPI * (sb + t) + lane / CPR;
+        if (row < g.M && col < g.N) store_stream(v[t], out + row * g.N + col);
+      }
+    }
   }
 }
 

@@ -287,9 +287,9 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   static_assert(ROWS * UNITS % THREADS == 0 && THREADS / UNITS % 16 == 0, "load split");
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE + BM * 8 + BN * 12];
   float* const lds_sx = reinterpret_cast<float*>(smem + 2 * STAGE);
-  int32_t* const lds_z = reinterpret_cast<int32_t*>(smem + 2 * STAGE + BM * 4);
+  float* const lds_z = reinterpret_cast<float*>(smem + 2 * STAGE + BM * 4);
   float* const lds_sw = reinterpret_cast<float*>(smem + 2 * STAGE + BM * 8);
-  int32_t* const lds_sum = reinterpret_cast<int32_t*>(smem + 2 * STAGE + BM * 8 + BN * 4);
+  float* const lds_sum = reinterpret_cast<float*>(smem + 2 * STAGE + BM * 8 + BN * 4);
   float* const lds_b = reinterpret_cast<float*>(smem + 2 * STAGE + BM * 8 + BN * 8);
 
   const int tid = threadIdx.x;
@@ -445,11 +445,11 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   if (tid < BM) {
     // Staged pre-scaled for the epilogue: sx / 256 and (8 - zx) * 256 (exact).
     lds_sx[tid] = meta_sx * 0.00390625f;
-    lds_z[tid] = (8 - meta_z) * 256;
+    lds_z[tid] = (float)((8 - meta_z) * 256);
   }
   if (tid < BN) {
     lds_sw[tid] = meta_sw;
-    lds_sum[tid] = meta_sum;
+    lds_sum[tid] = (float)meta_sum;
     if (BIAS) lds_b[tid] = meta_b;
   }
   lstore(G0, 0, C0{}, C3{});
@@ -505,14 +505,54 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     unpack_step(U0, 0);
     interleave();
   };
+  // The last slice: its fragments only (units 2, 3 read at steps 1, 3); no
+  // next slice to load, store, publish or read.
+  auto last_slice = [&](int s) {
+    const int cbuf = s & 1;
+    mfma_step(U0);
+    unpack_step(U1, 1);
+    interleave();
+    mfma_step(U1);
+    unpack_step(U0, 2);
+    lread(cbuf, 2);
+    interleave();
+    mfma_step(U0);
+    unpack_step(U1, 3);
+    interleave();
+    mfma_step(U1);
+    unpack_step(U0, 4);
+    lread(cbuf, 3);
+    interleave();
+    mfma_step(U0);
+    unpack_step(U1, 5);
+    interleave();
+    mfma_step(U1);
+    unpack_step(U0, 6);
+    interleave();
+    mfma_step(U0);
+    unpack_step(U1, 7);
+    interleave();
+    mfma_step(U1);
+  };
   // Slice s + 1 sits in G1 when s is even, in G0 when s is odd.
-  slice(0, G1, G0, std::true_type{});
-  int s = 1;
-  for (; s + 1 < nslices; s += 2) {
-    slice(s, G0, G1, std::false_type{});
-    slice(s + 1, G1, G0, std::false_type{});
+  int s = 0;
+  if (nslices > 1) {
+    slice(0, G1, G0, std::true_type{});
+    s = 1;
+    for (; s + 2 < nslices; s += 2) {
+      slice(s, G0, G1, std::false_type{});
+      slice(s + 1, G1, G0, std::false_type{});
+    }
+    if (s + 1 < nslices) {
+      slice(s, G0, G1, std::false_type{});
+      ++s;
+    }
   }
-  if (s < nslices) slice(s, G0, G1, std::false_type{});
+  last_slice(s);
+  // The LDS stage of the last slice's neighbour, (s + 1) & 1, is idle: its
+  // slice's fragments were read before the barrier every wave passed in
+  // slice s - 1, and nothing was written to it since.
+  [[maybe_unused]] const int idle_buf = (s + 1) & 1;
 
   // ---- epilogue.  The MFMAs took B as their first operand, so acc[i][j] is
   // the transposed 32 x 32 tile: output row m, column n sits in lane
@@ -520,10 +560,12 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
   // therefore holds runs of 4 consecutive columns of one row and writes them
   // straight to memory (8 bytes fp16 / 16 bytes fp32).  Operation order of
   // kernel/w4a4.cu:74-77, with the row factors staged as sx / 256 and
-  // (8 - zx) * 256: corrected * 256 = acc + (8 - zx) * 256 * sums is one
-  // v_mad_i32_i24 (|(8 - zx) * 256| <= 2048 and |sums| < 2^23 fit 24 bits; the
-  // sum stays below 2^31 for K <= 65536), and float(corrected * 256) * (sx / 256)
-  // equals float(corrected) * sx exactly (power-of-two scalings).
+  // (8 - zx) * 256 and the column sums as floats: corrected * 256 =
+  // fma((8 - zx) * 256, sums, float(acc)) is exact for K <= 65536 (every term
+  // is an integer multiple of 256 below 2^31 with at most 24 significant bits:
+  // |acc / 256| <= 2^22, |(8 - zx) * sums| <= 2^22, |corrected| <= 2^23), and
+  // float(corrected * 256) * (sx / 256) equals float(corrected) * sx exactly
+  // (power-of-two scalings).
   // Row and column metadata were staged in LDS before the first barrier of
   // the K loop.
   const int rl = lane & 31;
@@ -546,65 +588,66 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
     return;
   }
   float sxr[FM];
-  int32_t zr[FM];
+  float zr[FM];
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     sxr[i] = lds_sx[wm * TM + i * 32 + rl];
     zr[i] = lds_z[wm * TM + i * 32 + rl];
   }
   float4 swc[FN][4], bc[FN][4];
-  int4 sumc[FN][4];
+  float4 sumc[FN][4];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int cl = wn * TN + j * 32 + 8 * q + cq;
       swc[j][q] = *reinterpret_cast<const float4*>(lds_sw + cl);
-      sumc[j][q] = *reinterpret_cast<const int4*>(lds_sum + cl);
+      sumc[j][q] = *reinterpret_cast<const float4*>(lds_sum + cl);
       if (BIAS) bc[j][q] = *reinterpret_cast<const float4*>(lds_b + cl);
     }
-  auto value = [&](int i, int j, int v, float sw, int32_t sum, float b) {
-    const int32_t corrected256 = mad_i24(zr[i], sum, acc[i][j][v]);
-    float res = (float)corrected256 * sxr[i];
+  auto value = [&](int i, int j, int v, float sw, float sum, float b) {
+    float res = fmaf(zr[i], sum, (float)acc[i][j][v]) * sxr[i];
     res = res * sw;
     if (BIAS) res = res + b;
     return res;
   };
   OutT* out = static_cast<OutT*>(g.out);
   // fp16 output without raw accumulators: each wave's TM x 64 tile passes
-  // through LDS (the slice buffers, idle once every wave is past the K loop)
-  // so that a store instruction writes 8 whole 128-byte row segments instead
-  // of 16-byte pieces of 32 rows (M=2048, N=4096: 2.1-2.6 us faster at every
-  // K; the 16 MiB of output then take ~3.2 us).  Rows in LDS are 128 bytes, 16-byte
-  // chunk c of row r stored at c ^ (r & 7), so 8 consecutive lanes -- 8 rows
-  // on the writes, one row on the reads -- cover all banks.
+  // through LDS so that a store instruction writes 8 whole 128-byte row
+  // segments instead of 16-byte pieces of 32 rows (M=2048, N=4096: 2.1-2.6 us
+  // faster at every K; the 16 MiB of output then take ~3.2 us).  Rows in LDS
+  // are 128 bytes, 16-byte chunk c of row r stored at c ^ (r & 7), so 8
+  // consecutive lanes -- 8 rows on the writes, one row on the reads -- cover
+  // all banks.
   if constexpr (sizeof(OutT) == 2 && TN == 64) {
     static_assert(WM * WN * TM * TN * 2 <= 2 * STAGE, "staged tiles fit the slice buffers");
+    static_assert(WM * WN * 32 * 128 <= STAGE, "a 32-row group per wave fits one stage");
     if (!g.raw) {
-      __syncthreads();
-      uint8_t* const tile = smem + wave * (TM * TN * 2);
-      // Rows i * 32 .. + 31 of the wave's tile into LDS.
-      auto stage_rows = [&](int i) {
+      // Rows i * 32 .. + 31 of the wave's tile into LDS, row i * 32 + r at
+      // dst + r * 128.
+      auto stage_rows = [&](int i, uint8_t* dst) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const float4 sw = swc[j][q];
-            const int4 sm = sumc[j][q];
+            const float4 sm = sumc[j][q];
             const float4 b = bc[j][q];
             uint2 pk;
             pk.x = pack_h2(value(i, j, 4 * q + 0, sw.x, sm.x, b.x),
                            value(i, j, 4 * q + 1, sw.y, sm.y, b.y));
             pk.y = pack_h2(value(i, j, 4 * q + 2, sw.z, sm.z, b.z),
                            value(i, j, 4 * q + 3, sw.w, sm.w, b.w));
-            const int lr = i * 32 + rl;
-            *reinterpret_cast<uint2*>(tile + lr * 128 + 16 * ((4 * j + q) ^ (rl & 7)) +
+            *reinterpret_cast<uint2*>(dst + rl * 128 + 16 * ((4 * j + q) ^ (rl & 7)) +
                                       8 * (lane >> 5)) = pk;
           }
       };
       if constexpr (GATED) {
+        // Whole tiles in the slice buffers, once every wave is past the K loop.
+        __syncthreads();
+        uint8_t* const tile = smem + wave * (TM * TN * 2);
 #pragma unroll
-        for (int i = 0; i < FM; ++i) stage_rows(i);
+        for (int i = 0; i < FM; ++i) stage_rows(i, tile + i * 32 * 128);
         // SiLU-gated MLP (weights interleaved in 64-row blocks: gate rows then
         // up rows of the same 64 outputs): the gate half of the tile's rows
         // is in the LDS tiles of waves (wm, 0), the up half in (wm, 1).  Wave
@@ -631,9 +674,13 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
         }
         return;
       }
-      // One 32-row group at a time: the group's stores go out while the next
-      // group is converted.  A wave reads back only what its own lanes wrote;
-      // the wave-scope fence orders their LDS writes before the reads.
+      // One 32-row group at a time through the wave's own 4 KiB of the idle
+      // stage (no workgroup barrier: no other wave touches it): the group's
+      // stores go out while the next group is converted.  A wave reads back
+      // only what its own lanes wrote; the wave-scope fences keep the LDS
+      // writes of a group after the reads of the previous one and before its
+      // own reads.
+      uint8_t* const tile = smem + idle_buf * STAGE + wave * (32 * 128);
       const int c8 = lane & 7;
       const int64_t col = n0 + wn * TN + 8 * c8;
       // A tile inside the output (every tile of a grid whose M and N are
@@ -642,24 +689,28 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
       // before its stores.
       const int wv = __builtin_amdgcn_readfirstlane(wave);
       const bool whole = m0 + BM <= g.M && n0 + BN <= g.N;
-      const uint8_t* const obase = reinterpret_cast<const uint8_t*>(out) +
-                                   2 * ((m0 + (wv / WN) * TM) * g.N + n0 + (wv % WN) * TN);
+      uint8_t* const obase = reinterpret_cast<uint8_t*>(out) +
+                             2 * ((m0 + (wv / WN) * TM) * g.N + n0 + (wv % WN) * TN);
       const uint32_t lane_off = (uint32_t)(2 * ((lane >> 3) * g.N + 8 * c8));
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        stage_rows(i);
+        if (i > 0) {
+          __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+        }
+        stage_rows(i, tile);
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         __builtin_amdgcn_wave_barrier();
         uint4 v[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const int lr = i * 32 + 8 * s + (lane >> 3);
+          const int lr = 8 * s + (lane >> 3);
           v[s] = *reinterpret_cast<const uint4*>(tile + lr * 128 + 16 * (c8 ^ (lr & 7)));
         }
         if (whole) {
 #pragma unroll
           for (int s = 0; s < 4; ++s)
-            store_stream(v[s], const_cast<uint8_t*>(obase) + 2 * (i * 32 + 8 * s) * g.N + lane_off);
+            store_stream(v[s], obase + 2 * (i * 32 + 8 * s) * g.N + lane_off);
         } else {
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
@@ -680,7 +731,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINB) void w4a4_gemm_pipe_kernel(Gemm
       for (int q = 0; q < 4; ++q) {
         const int64_t c0 = n0 + wn * TN + j * 32 + 8 * q + cq;
         const float4 sw = swc[j][q];
-        const int4 sm = sumc[j][q];
+        const float4 sm = sumc[j][q];
         const float4 b = bc[j][q];
         const float r0 = value(i, j, 4 * q + 0, sw.x, sm.x, b.x);
         const float r1 = value(i, j, 4 * q + 1, sw.y, sm.y, b.y);

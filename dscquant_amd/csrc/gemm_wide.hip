@@ -40,13 +40,15 @@
 // 8 bytes k-step 2q + 1, the same for A and B, so every product pairs equal k.
 //
 // Epilogue: the scale and zero-point factors are staged pre-multiplied, sx / 256
-// and (8 - zx) * 256, so corrected * 256 = acc + (8 - zx) * 256 * sums is one
-// v_mad_i32_i24 and float(corrected * 256) * (sx / 256) equals
-// float(corrected) * sx exactly (power-of-two scalings, no overflow: |acc| <=
-// 2^30 and |corrected| < 2^23 for K <= 65536); then * sw (+ bias) and one fp16
-// rounding (v_cvt_pk_f16_f32), the reference's operation order.  Each wave's
-// 128 x BN/2 fp16 tile goes through LDS (the idle slice stages) so that every
-// store instruction writes whole row segments (four of 256 bytes at BN = 256).
+// and (8 - zx) * 256, and the column sums as floats, so corrected * 256 =
+// fma((8 - zx) * 256, sums, float(acc)) is exact (integers below 2^31 with at
+// most 24 significant bits: |acc / 256| <= 2^22 and |corrected| <= 2^23 for
+// K <= 65536) and float(corrected * 256) * (sx / 256) equals
+// float(corrected) * sx exactly (power-of-two scalings); then * sw (+ bias)
+// and one fp16 rounding (v_cvt_pk_f16_f32), the reference's operation order.
+// Each wave's 128 x BN/2 fp16 tile goes through LDS (the idle slice stages)
+// so that every store instruction writes whole row segments (four of 256
+// bytes at BN = 256).
 
 #include <type_traits>
 
@@ -97,9 +99,9 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   static_assert(kDma % 2 == 0, "the per-lane DMA offset pairs with the parity of j");
   __shared__ __attribute__((aligned(16))) uint8_t smem[kStages + kTileM * 8 + BN * 12];
   float* const lds_sx = reinterpret_cast<float*>(smem + kStages);             // sx / 256
-  int32_t* const lds_z = reinterpret_cast<int32_t*>(smem + kStages + kTileM * 4);  // (8 - zx) * 256
+  float* const lds_z = reinterpret_cast<float*>(smem + kStages + kTileM * 4);  // (8 - zx) * 256
   float* const lds_sw = reinterpret_cast<float*>(smem + kStages + kTileM * 8);
-  int32_t* const lds_sum = reinterpret_cast<int32_t*>(smem + kStages + kTileM * 8 + BN * 4);
+  float* const lds_sum = reinterpret_cast<float*>(smem + kStages + kTileM * 8 + BN * 4);
   float* const lds_b = reinterpret_cast<float*>(smem + kStages + kTileM * 8 + BN * 8);
 
   const int tid = threadIdx.x;
@@ -230,10 +232,10 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
       BIAS ? __half2float(static_cast<const __half*>(g.bias)[min(n0 + tid, g.N - 1)]) : 0.0f;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // slice 0 and the metadata
   lds_sx[tid] = meta_sx * 0.00390625f;                // exact: a power-of-two scaling
-  lds_z[tid] = (8 - meta_z) * 256;
+  lds_z[tid] = (float)((8 - meta_z) * 256);
   if (tid < BN) {
     lds_sw[tid] = meta_sw;
-    lds_sum[tid] = meta_sum;
+    lds_sum[tid] = (float)meta_sum;
     if (BIAS) lds_b[tid] = meta_b;
   }
   if (nslices > 1) dma(1, 1);
@@ -317,7 +319,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   __syncthreads();
   const int rl = lane & 31;
   float sxr[FM];
-  int32_t zr[FM];
+  float zr[FM];
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     sxr[i] = lds_sx[wm * 128 + i * 32 + rl];
@@ -337,16 +339,16 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
     for (int q = 0; q < 4; ++q) {
       const int cl = wn * TN + j * 32 + 8 * q + 4 * (lane >> 5);
       const float4 sw = *reinterpret_cast<const float4*>(lds_sw + cl);
-      const int4 sm = *reinterpret_cast<const int4*>(lds_sum + cl);
+      const float4 sm = *reinterpret_cast<const float4*>(lds_sum + cl);
       float4 bv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if (BIAS) bv = *reinterpret_cast<const float4*>(lds_b + cl);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const v16i& a = acc[i][j];
-        float r0 = (float)mad_i24(zr[i], sm.x, a[4 * q + 0]) * sxr[i];
-        float r1 = (float)mad_i24(zr[i], sm.y, a[4 * q + 1]) * sxr[i];
-        float r2 = (float)mad_i24(zr[i], sm.z, a[4 * q + 2]) * sxr[i];
-        float r3 = (float)mad_i24(zr[i], sm.w, a[4 * q + 3]) * sxr[i];
+        float r0 = fmaf(zr[i], sm.x, (float)a[4 * q + 0]) * sxr[i];
+        float r1 = fmaf(zr[i], sm.y, (float)a[4 * q + 1]) * sxr[i];
+        float r2 = fmaf(zr[i], sm.z, (float)a[4 * q + 2]) * sxr[i];
+        float r3 = fmaf(zr[i], sm.w, (float)a[4 * q + 3]) * sxr[i];
         r0 = r0 * sw.x;
         r1 = r1 * sw.y;
         r2 = r2 * sw.z;

@@ -53,15 +53,4 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, h2));
 }
 
-// c + a * b as one v_mad_i32_i24, which multiplies the low 24 bits of a and b
-// as signed values.  Only for operands known to fit 24 signed bits (the
-// epilogue's (8 - zx) * 256 and code sums, |b| < 2^20 for K <= 65536): with
-// __mul24 the compiler, not knowing that range, sign-extends every operand
-// first (one v_bfe_i32 each).
-__device__ __forceinline__ int32_t mad_i24(int32_t a, int32_t b, int32_t c) {
-  int32_t r;
-  asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-
 }  // namespace dscq

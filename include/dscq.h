@@ -273,9 +273,10 @@ int dscq_time_next_kernel(void* start, void* stop);
  * GEMM kernel choice for this thread's later dscq_matmul / dscq_matmul_ws /
  * dscq_matmul_noalloc calls (no reference counterpart; the analogue of the
  * reference's force_decode for the dense kernels, for tests and measurement):
- *   0  automatic (the default): the wide-tile kernel (256 x 256 tiles, one
- *      wave per SIMD) for fp16 output without raw accumulators when its tiles
- *      make at least two rounds of one tile per compute unit, else the
+ *   0  automatic (the default): for fp16 output without raw accumulators the
+ *      wide-tile kernel (256 x 256 tiles, one wave per SIMD) when its tiles
+ *      fill at least three quarters of a round of one tile per compute unit
+ *      and its rounds take no longer than the pipelined kernel's, else the
  *      pipelined kernel;
  *   1  the wide-tile kernel wherever it applies (fp16 output, no raw
  *      accumulators, N % 8 == 0, K a multiple of 256, KP <= 65536, M >= 64),

@@ -3,7 +3,8 @@ times it: every replay must read the current contents of its input buffers and
 give, bit for bit, what eager calls give on the same data.  Each replay is
 followed by eager work on the same stream and a synchronisation, and the inputs
 change between replays.  Covered: rotate+quantize+pack -> pipelined GEMM
-(prefill shape class, the prefill shape itself), quantize -> skinny-M GEMM (16
+(prefill shape class, the prefill shape itself) and -> wide-tile GEMM (forced
+at both tile widths, and by the automatic rule), quantize -> skinny-M GEMM (16
 tokens, one and three column tiles per workgroup), the fused decode kernel (one
 and three tiles per workgroup, both product forms), and the SiLU-gated
 requantization.
@@ -59,6 +60,30 @@ def test_quantize_matmul_graph(gpu, M, K, N):
 
     xs = [torch.from_numpy(activations(M, K, seed=s).astype(np.float16)).to(gpu)
           for s in (1, 2, 3)]
+    _replay_and_compare(run, xs)
+
+
+@pytest.mark.parametrize("M,K,N,which,use_bias", [(512, 4096, 2048, 3, False),
+                                                   (300, 2048, 1032, 4, True),
+                                                   (4096, 4096, 4096, 0, False)])
+def test_quantize_wide_matmul_graph(gpu, M, K, N, which, use_bias):
+    """The wide-tile GEMM (LDS DMA) captured and replayed: forced with 256 x 256
+    or 256 x 128 tiles, and chosen by the automatic rule at 4096 x 4096 x 4096."""
+    from tests.test_gpu_wide import gemm_kernel
+    print(f"graph quantize+wide matmul M{M} K{K} N{N} kernel{which} bias{use_bias}", flush=True)
+    pw, sw, sums = w4a4.pack_weight(torch.from_numpy(weights(N, K, seed=12)).to(gpu), 1.0, 128)
+    bias = (torch.from_numpy((np.random.default_rng(1).standard_normal(N) * 0.1)
+                             .astype(np.float16)).to(gpu) if use_bias
+            else torch.empty(0, dtype=torch.float16, device=gpu))
+
+    def run(x):
+        with gemm_kernel(which):
+            pa, sx, zx = w4a4.quantize(x, 1.0, True, 128)
+            out, _ = w4a4.matmul(pa, pw, sx, zx, sw, sums, bias, M, N)
+        return [out, pa, sx, zx]
+
+    xs = [torch.from_numpy(activations(M, K, seed=s).astype(np.float16)).to(gpu)
+          for s in (7, 8, 9)]
     _replay_and_compare(run, xs)
 
 

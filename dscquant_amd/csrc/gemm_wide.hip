@@ -317,7 +317,11 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   // its last (redundant) DMA has landed.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  const int rl = lane & 31;
+  // The epilogue's lane-derived indices are computed here from the lane's own
+  // position (mbcnt over all lanes), not kept live across the K loop, which
+  // holds 256 VGPRs and would spill them.
+  const int el = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int rl = el & 31;
   float sxr[FM];
   float zr[FM];
 #pragma unroll
@@ -332,12 +336,12 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   // reads cover them.
   constexpr int RB = 2 * TN, CPR = TN / 8, LCPR = CPR == 16 ? 4 : 3, RPI = 64 / CPR;
   uint8_t* const tile = smem + wave * (128 * RB);
-  const int half = ((lane >> 5) ^ (rl >> LCPR)) & 1;
+  const int half = ((el >> 5) ^ (rl >> LCPR)) & 1;
 #pragma unroll
   for (int j = 0; j < FN; ++j)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int cl = wn * TN + j * 32 + 8 * q + 4 * (lane >> 5);
+      const int cl = wn * TN + j * 32 + 8 * q + 4 * (el >> 5);
       const float4 sw = *reinterpret_cast<const float4*>(lds_sw + cl);
       const float4 sm = *reinterpret_cast<const float4*>(lds_sum + cl);
       float4 bv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -371,7 +375,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __half* const out = static_cast<__half*>(g.out);
-  const int c = lane % CPR;
+  const int c = el % CPR;
   const int64_t col = n0 + wn * TN + 8 * c;
   // A tile inside the output stores without per-row tests: a wave-uniform row
   // base plus a 32-bit lane offset, the LDS reads of eight store instructions
@@ -379,7 +383,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   const bool whole = m0 + kTileM <= g.M && n0 + BN <= g.N;
   uint8_t* const obase =
       reinterpret_cast<uint8_t*>(out) + 2 * ((m0 + wm * 128) * g.N + n0 + wn * TN);
-  const uint32_t out_off = (uint32_t)(2 * ((lane / CPR) * g.N + 8 * c));
+  const uint32_t out_off = (uint32_t)(2 * ((el / CPR) * g.N + 8 * c));
   constexpr int kBatch = 8;
 #pragma unroll
   for (int sb = 0; sb < 128 / RPI; sb += kBatch) {
@@ -387,7 +391,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
 #pragma unroll
     for (int t = 0; t < kBatch; ++t) {
       const int sr = sb + t;
-      const int r = RPI * sr + lane / CPR;
+      const int r = RPI * sr + el / CPR;
       v[t] = *reinterpret_cast<const uint4*>(tile + r * RB + 16 * (c ^ (r & (CPR - 1))));
       if ((sr >> (2 * LCPR - 6)) & 1) {  // bit log2(CPR) of r: halves stored swapped
         const uint32_t x = v[t].x, y = v[t].y;
@@ -404,7 +408,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
     } else {
 #pragma unroll
       for (int t = 0; t < kBatch; ++t) {
-        const int64_t row = m0 + wm * 128 + RPI * (sb + t) + lane / CPR;
+        const int64_t row = m0 + wm * 128 + RPI * (sb + t) + el / CPR;
         if (row < g.M && col < g.N) store_stream(v[t], out + row * g.N + col);
       }
     }

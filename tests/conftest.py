@@ -29,6 +29,15 @@ def _oracle_built():
         native.build()
 
 
+def sweep_size(n: int, seed: int):
+    """(case count, seed) of a seeded random sweep.  DSCQ_SWEEP_SEED (added to
+    every sweep's own seed) and DSCQ_SWEEP_SCALE (multiplying its case count)
+    draw other or more cases; unset, every sweep keeps its committed cases."""
+    shift = int(os.environ.get("DSCQ_SWEEP_SEED", "0"))
+    scale = float(os.environ.get("DSCQ_SWEEP_SCALE", "1"))
+    return max(1, int(round(n * scale))), seed + shift
+
+
 def activations(M: int, K: int, seed: int = 0, outlier_frac: float = 0.01,
                 outlier_scale: float = 50.0, dtype=np.float16) -> np.ndarray:
     """X ~ N(0,1) [M, K] with ceil(1%) of channels (seeded choice) scaled x50."""

@@ -14,7 +14,7 @@ import torch
 
 from dscquant_amd import w4a4
 from oracle import native
-from tests.conftest import activations, weights
+from tests.conftest import activations, weights, sweep_size
 
 pytestmark = pytest.mark.gpu
 
@@ -46,7 +46,7 @@ def _cases(n, seed):
     return out
 
 
-CASES = _cases(28, seed=31337)
+CASES = _cases(*sweep_size(28, 31337))
 
 
 @pytest.mark.parametrize("M,K,N,rot,clip,x32,bias,fp32", CASES,

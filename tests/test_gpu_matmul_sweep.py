@@ -14,6 +14,7 @@ import torch
 
 from dscquant_amd import w4a4
 from oracle import native
+from tests.conftest import sweep_size
 from tests.test_gpu_matmul import _operands, _oracle_raw
 
 pytestmark = pytest.mark.gpu
@@ -37,7 +38,7 @@ def _cases(n, seed):
     return out
 
 
-CASES = _cases(48, seed=2026)
+CASES = _cases(*sweep_size(48, 2026))
 
 
 @pytest.mark.parametrize("M,N,K,use_bias,fp32,force_decode", CASES,

@@ -17,7 +17,7 @@ import torch
 
 from dscquant_amd import w4a4
 from oracle import native
-from tests.conftest import activations, weights
+from tests.conftest import activations, weights, sweep_size
 
 pytestmark = pytest.mark.gpu
 
@@ -42,7 +42,7 @@ def _cases(n, seed):
     return out
 
 
-CASES = _cases(40, seed=4242)
+CASES = _cases(*sweep_size(40, 4242))
 
 
 @pytest.mark.parametrize("M,K,rot,clip,dtype,fused", CASES,

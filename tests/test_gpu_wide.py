@@ -5,7 +5,8 @@ its tile width, for any shape it applies to).
 Its fp16 outputs are compared bit for bit with the oracle's epilogue on the
 oracle's int32 accumulators (kernel/w4a4.cu:70-161) at ragged shapes (partial
 tiles in M and N, one to five K slices, tiny M), with and without bias, and
-with the largest accumulator and zero-point-correction magnitudes; at the
+with the largest accumulator and zero-point-correction magnitudes, and at
+seeded random shapes inside its contract; at the
 70B shapes, where the automatic choice takes it, its whole output is compared
 with the pipelined kernel's (itself checked against the oracle there).
 """
@@ -15,6 +16,7 @@ import torch
 
 from dscquant_amd import _lib, w4a4
 from oracle import native
+from tests.conftest import sweep_size
 from tests.test_gpu_matmul import _dequant64, _operands, _oracle_raw
 
 pytestmark = pytest.mark.gpu
@@ -72,6 +74,30 @@ def test_wide_kernel_matches_oracle(gpu, M, N, K, use_bias, width):
     rel = np.abs(got.astype(np.float64) - exact) / np.maximum(np.abs(exact), 1e-30)
     big = np.abs(exact) > 1e-2
     assert rel[big].max() <= 1e-3
+
+
+def _random_cases(n, seed):
+    """Seeded shapes inside the wide kernel's contract (N % 8 == 0, K a
+    multiple of 256): ragged M and N, 1-39 slices, either tile width."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        M = int(rng.integers(1, 1400))
+        N = int(rng.integers(1, 1600)) * 8
+        K = int(rng.integers(1, 40)) * 256
+        if M * N * K > 2.0e9:
+            continue
+        out.append((M, N, K, bool(rng.random() < 0.5), int(rng.choice([256, 128]))))
+    return out
+
+
+RANDOM_CASES = _random_cases(*sweep_size(12, 8086))
+
+
+@pytest.mark.parametrize("M,N,K,use_bias,width", RANDOM_CASES,
+                         ids=[f"M{c[0]}-N{c[1]}-K{c[2]}-w{c[4]}" for c in RANDOM_CASES])
+def test_wide_kernel_random_shapes(gpu, M, N, K, use_bias, width):
+    test_wide_kernel_matches_oracle(gpu, M, N, K, use_bias, width)
 
 
 @pytest.mark.parametrize("width", [256, 128])

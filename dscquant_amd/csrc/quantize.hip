@@ -48,6 +48,13 @@ constexpr int kThreads = 256;
 // 512 x 8192 equal (5.74 / 5.76).
 constexpr int64_t kSpreadMaxRows = 512;
 constexpr int kSpreadMaxPasses = 3;
+// Rows from which the few-row kernel computes each row's scale in one wave and
+// shares it (RowArgs::share_scale).  Graph-replayed, rotation 128, identical
+// codes, every wave / one wave: 512 x 4096 3.84-4.03 / 3.68-3.90 us, 512 x
+// 11008 6.63-6.70 / 6.46-6.51; 8-256 rows equal within 0.05 us (the decode
+// step at 8 rows measured 2% slower with the extra barrier, so fewer rows
+// keep the per-wave form).
+constexpr int64_t kShareScaleRows = 128;
 
 struct RowArgs {
   const void* x;       // [M, K] T
@@ -61,6 +68,7 @@ struct RowArgs {
   int32_t* zeros;      // [MP] act zero-points or null
   int32_t* sums;       // [MP] weight code sums or null
   int vec;             // rows 16-byte aligned and K % 8 == 0
+  int share_scale = 0; // few-row kernel: one wave computes the row scale for all
   int64_t ldx;         // elements between consecutive rows of x (and up)
   const void* up;      // gated input: up [M, ldx] fp16, or null
   __half* hout;        // gated input: the activation h [M, K] fp16, or null
@@ -277,6 +285,7 @@ __global__ __launch_bounds__(TPB) void row_quant_kernel(RowArgs a) {
   }
   if (MODE == kAct) mn = wave_min(mn);
   mx = wave_max(mx);
+  RowScale rs;
   if (WPR > 1) {
     __shared__ float red[2][TPB / 64];
     if (lane == 0) {
@@ -284,15 +293,45 @@ __global__ __launch_bounds__(TPB) void row_quant_kernel(RowArgs a) {
       red[1][wave] = mx;
     }
     __syncthreads();
-    mn = red[0][row_in_wg * WPR];
-    mx = red[1][row_in_wg * WPR];
+    auto fold = [&]() {
+      mn = red[0][row_in_wg * WPR];
+      mx = red[1][row_in_wg * WPR];
 #pragma unroll
-    for (int w = 1; w < WPR; ++w) {
-      mn = fminf(mn, red[0][row_in_wg * WPR + w]);
-      mx = fmaxf(mx, red[1][row_in_wg * WPR + w]);
+      for (int w = 1; w < WPR; ++w) {
+        mn = fminf(mn, red[0][row_in_wg * WPR + w]);
+        mx = fmaxf(mx, red[1][row_in_wg * WPR + w]);
+      }
+    };
+    if constexpr (MODE == kAct) {
+      // The row's first wave folds the statistics and computes the scale,
+      // zero point, reciprocal and guard (two IEEE divisions, ~50 VALU
+      // instructions) once for the row; the other waves read them, leaving
+      // their SIMDs to other rows' waves meanwhile.  Same values as every
+      // wave computing them: the same inputs in the same order.
+      __shared__ float rsh[ROWS][4];
+      if (wave_in_row == 0) {
+        fold();
+        rs = row_scale<MODE>(mn, mx, a.clip, a.qmax);
+        if (lane == 0) {
+          rsh[row_in_wg][0] = rs.scale;
+          rsh[row_in_wg][1] = rs.y;
+          rsh[row_in_wg][2] = rs.zf;
+          rsh[row_in_wg][3] = rs.thr;
+        }
+      }
+      __syncthreads();
+      rs.scale = rsh[row_in_wg][0];
+      rs.y = rsh[row_in_wg][1];
+      rs.zf = rsh[row_in_wg][2];
+      rs.thr = rsh[row_in_wg][3];
+      rs.qmax = a.qmax;
+    } else {
+      fold();
+      rs = row_scale<MODE>(mn, mx, a.clip, a.qmax);
     }
+  } else {
+    rs = row_scale<MODE>(mn, mx, a.clip, a.qmax);
   }
-  RowScale rs = row_scale<MODE>(mn, mx, a.clip, a.qmax);
   // The zero point and the guard threshold are uniform over the wave: keep
   // them in scalar registers (operands of every chunk's fma and compare).
   rs.zf = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, rs.zf)));
@@ -597,14 +636,44 @@ __global__ __launch_bounds__(512) void row_quant_spread_kernel(RowArgs a) {
     red[1][wave] = mx;
   }
   __syncthreads();
-  mn = red[0][0];
-  mx = red[1][0];
+  auto fold = [&]() {
+    mn = red[0][0];
+    mx = red[1][0];
 #pragma unroll
-  for (int k = 1; k < 8; ++k) {
-    mn = fminf(mn, red[0][k]);
-    mx = fmaxf(mx, red[1][k]);
+    for (int k = 1; k < 8; ++k) {
+      mn = fminf(mn, red[0][k]);
+      mx = fmaxf(mx, red[1][k]);
+    }
+  };
+  RowScale rs;
+  if (a.share_scale) {
+    // Many rows (the SIMDs hold several workgroups): wave 0 folds the
+    // statistics and computes the row's scale, zero point, reciprocal and
+    // guard once (~50 VALU instructions) and the other waves read them,
+    // leaving their SIMDs to other rows.  With few rows every wave computes
+    // them itself, which spares the latency of a second barrier.  Same values
+    // either way: the same inputs in the same order.
+    __shared__ float rsh[4];
+    if (wave == 0) {
+      fold();
+      const RowScale r0 = row_scale<kAct>(mn, mx, a.clip, a.qmax);
+      if (lane == 0) {
+        rsh[0] = r0.scale;
+        rsh[1] = r0.y;
+        rsh[2] = r0.zf;
+        rsh[3] = r0.thr;
+      }
+    }
+    __syncthreads();
+    rs.scale = rsh[0];
+    rs.y = rsh[1];
+    rs.zf = rsh[2];
+    rs.thr = rsh[3];
+    rs.qmax = a.qmax;
+  } else {
+    fold();
+    rs = row_scale<kAct>(mn, mx, a.clip, a.qmax);
   }
-  const RowScale rs = row_scale<kAct>(mn, mx, a.clip, a.qmax);
   RowScale rs_l = rs;
   rs_l.y = lsign * rs.y;
 #pragma unroll
@@ -801,6 +870,7 @@ int row_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t MP, float 
   if (mode == kAct && a.vec && a.nblk <= 32 * kSpreadMaxPasses && MP <= kSpreadMaxRows) {
     const bool noclamp = clip == 1.0f && qmax == 15.0f;
     const int passes = (a.nblk + 31) / 32;
+    a.share_scale = MP >= kShareScaleRows;
 #define DSCQ_SPREAD_P(T, R, C)                                                                  \
   if (passes == 1)                                                                              \
     launch((row_quant_spread_kernel<T, R, C, 1>), dim3((unsigned)MP), dim3(512), stream, a);    \

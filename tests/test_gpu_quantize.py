@@ -120,6 +120,31 @@ def test_quantize_special_rows(gpu):
                 np.testing.assert_array_equal(g.cpu().numpy(), r)
 
 
+@pytest.mark.parametrize("M,K,rot", [(256, 4096, 0), (256, 4096, 128), (2048, 4096, 128),
+                                     (600, 8192, 128), (4096, 8192, 0)])
+def test_quantize_special_rows_where_one_wave_computes_the_scale(gpu, M, K, rot):
+    """The same special rows, repeated over shapes whose rows span several waves
+    (the few-row kernel from 128 rows, the register kernel with two or four
+    waves per row), where one wave of the row computes its scale for the
+    others, next to rows of ordinary data."""
+    print(f"special rows case M{M} K{K} rot{rot}", flush=True)
+    base = activations(M, K, seed=M + K + rot, dtype=np.float32)
+    x = base.copy()
+    x[0::7] = 0.0
+    x[1::7] = 3.0
+    x[2::7] = np.linspace(0.1, 2.0, K, dtype=np.float32)
+    x[3::7] = -np.linspace(0.1, 2.0, K, dtype=np.float32)
+    x[4::7] = np.linspace(-1.0, 1.0, K, dtype=np.float32)
+    x[5::7] = 0.0
+    x[5::7, 17] = -1e-3
+    xd = x.astype(np.float16)
+    got = w4a4.quantize(torch.from_numpy(xd).to(gpu), 1.0, True, rot)
+    torch.cuda.synchronize()
+    ref = native.quantize_rows(xd.astype(np.float32), 1.0, rot)
+    for g, r in zip(got, ref):
+        np.testing.assert_array_equal(g.cpu().numpy(), r)
+
+
 def _tie_rows(rows: int, K: int, zero: int = 0) -> np.ndarray:
     """Rows whose x / scale + zero land exactly on j + .5.
 

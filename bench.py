@@ -256,6 +256,14 @@ def gemm_kernel_name(M, N, K, choice, cus=256):
     return "w4a4_gemm_wide_kernel<256>" if choice == "wide" else "w4a4_gemm_pipe_kernel"
 
 
+def gated_kernel_name(M, NH, K, choice, cus=256):
+    """The kernel dscq_matmul_silu_mul takes for M > 16 (the library's rule,
+    restated): the wide-tile kernel by the dense rule at 256 x 256 tiles, else
+    the pipelined kernel (the gated GEMM has no 256 x 128 wide form)."""
+    name = gemm_kernel_name(M, 2 * NH, K, choice, cus)
+    return name if name == "w4a4_gemm_wide_kernel<256>" else "w4a4_gemm_pipe_kernel"
+
+
 def traffic_summary(fetch_csv, write_csv):
     """Mean FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel class, scaled by the
     ratio of bytes a 16 MiB device copy really moves to what the counter reports for it."""
@@ -933,7 +941,7 @@ def main_mlp(args, torch, _lib, w4a4):
     line = {"bound": "mfma", "achieved": round(gu_ops / tg / 1e12, 2),
             "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
             "frac": round(gu_ops / tg / 1e12 / PEAK_INT8_TOPS, 4),
-            "kernel": "w4a4_gemm_pipe_kernel (gate|up, SiLU-gated epilogue)",
+            "kernel": gated_kernel_name(M, N, K, args.gemm_kernel) + " (gate|up, SiLU-gated epilogue)",
             "avg_us": round(tg * 1e6, 3),
             "isolated_us": round(t_iso["gemm_gate_up_silu"] * 1e6, 3),
             "ops_per_launch": gu_ops, "traffic": None}

@@ -1161,6 +1161,19 @@ int use_wide(const GemmArgs& g, bool out_half) {
   return pref == 1 ? 256 : 0;
 }
 
+// The gated GEMM of dscq_matmul_silu_mul on the wide-tile kernel (256 x 256
+// tiles; each wave's 128 columns are the gate and up rows of 64 outputs), by
+// the rule of use_wide; preferences 1 and 3 take it wherever it applies, 2
+// and 4 never.  Gated GEMM alone, graph-replayed, identical h, pipelined /
+// wide (M x N/2, K = 4096 unless noted): 512 x 14336 55.4-62.4 / 49.6-53.2
+// us; 2048 x 11008 176.5-199.2 / 154.0-160.2; 4096 x 11008 312-331 /
+// 294-304; 2048 x 28672, K = 8192 688-714 / 621-631; left to the pipelined
+// kernel by the rule: 512 x 11008 49.9-53.6 / 49.1-51.5; 1024 x 11008
+// 85.6-97.6 / 98.1-99.6; 256 x 11008 25.9-27.8 / 44.6-46.3.
+bool use_wide_gated(const GemmArgs& g) {
+  return g.N % 128 == 0 && use_wide(g, true) == 256;
+}
+
 template <typename OutT>
 int gemm_typed(const GemmArgs& g, bool decode, int32_t* ws, int64_t ws_bytes,
                hipStream_t stream) {
@@ -1286,6 +1299,7 @@ int w4a4_gemm_silu_mul(const uint8_t* a, const uint8_t* b_gu, const float* sx,
   // rows it keeps doing so unless the pipelined kernel has 64+ tiles (as for
   // dscq_matmul).
   if (M <= 16 || (M < 64 && !use_pipe_mid_m(g, true))) return launch_gemv<__half, true>(g, stream);
+  if (use_wide_gated(g)) return launch_wide_gemm_gated(g, stream);
   return launch_pipe<__half, true>(g, stream);
 }
 

@@ -35,6 +35,10 @@ struct GemmArgs {
 // launch_wide_gemm runs it.
 bool wide_gemm_fits(const GemmArgs& g);
 int launch_wide_gemm(GemmArgs g, int bn, hipStream_t stream);
+// The same kernel with 256 x 256 tiles and the SiLU-gated epilogue of
+// dscq_matmul_silu_mul (gate and up rows interleaved in blocks of 64, h
+// [M, N / 2] fp16 out).
+int launch_wide_gemm_gated(GemmArgs g, hipStream_t stream);
 
 // This thread's GEMM kernel preference (dscq_set_gemm_kernel): 0 automatic,
 // 1 the wide-tile kernel wherever it applies, 2 never, 3 / 4 the wide-tile

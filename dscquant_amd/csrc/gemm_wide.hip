@@ -56,6 +56,7 @@
 #include "common.h"
 #include "gemm_args.h"
 #include "mma_int4.h"
+#include "rowquant.h"
 
 namespace dscq {
 namespace {
@@ -88,7 +89,7 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
 }
 #pragma clang diagnostic pop
 
-template <int BN, bool BIAS>
+template <int BN, bool BIAS, bool GATED = false>
 __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs g) {
   // 2 x 2 waves, each 128 x (BN / 2): 4 x FN MFMA tiles.
   constexpr int FM = 4, FN = BN / 64, NF = FM + FN, TN = BN / 2, MF = FM * FN;
@@ -96,6 +97,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
   constexpr int kStages = kBRegion + 2 * kHalfB;
   constexpr int kDma = (kTileM + BN) / 8 / kWaves;  // DMA instructions per wave per slice
   static_assert(BN == 256 || BN == 128, "tile width");
+  static_assert(!GATED || BN == 256, "gated tiles pair gate and up rows within a wave's 128 columns");
   static_assert(kDma % 2 == 0, "the per-lane DMA offset pairs with the parity of j");
   __shared__ __attribute__((aligned(16))) uint8_t smem[kStages + kTileM * 8 + BN * 12];
   float* const lds_sx = reinterpret_cast<float*>(smem + kStages);             // sx / 256
@@ -329,6 +331,99 @@ __global__ __launch_bounds__(64 * kWaves, 1) void w4a4_gemm_wide_kernel(GemmArgs
     sxr[i] = lds_sx[wm * 128 + i * 32 + rl];
     zr[i] = lds_z[wm * 128 + i * 32 + rl];
   }
+  if constexpr (GATED) {
+    // SiLU-gated MLP (dscq_matmul_silu_mul): the weight rows are interleaved in
+    // blocks of 64 -- gate rows of 64 outputs, then the up rows of the same
+    // outputs -- so a wave's 128 columns hold gate (MFMA tiles j = 0, 1) and up
+    // (j = 2, 3) of 64 outputs, element for element in the same lane and
+    // register.  Each pair is narrowed to fp16 as the GEMM output would be and
+    // combined into h = silu_mul_f16x2(g, u) (rowquant.h, the arithmetic of
+    // the pipelined kernel's gated epilogue and of the requantizing kernel);
+    // the wave's 128 x 64 h tile goes through LDS (rows of 128 bytes, the
+    // 128-column layout of the plain epilogue) and out to h [M, N / 2].
+    constexpr int HRB = 128, HCPR = 8, HRPI = 8;
+    uint8_t* const tile = smem + wave * (128 * HRB);
+    const int half = ((el >> 5) ^ (rl >> 3)) & 1;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int cg = wn * TN + j * 32 + 8 * q + 4 * (el >> 5), cu = cg + 64;
+        const float4 swg = *reinterpret_cast<const float4*>(lds_sw + cg);
+        const float4 smg = *reinterpret_cast<const float4*>(lds_sum + cg);
+        const float4 swu = *reinterpret_cast<const float4*>(lds_sw + cu);
+        const float4 smu = *reinterpret_cast<const float4*>(lds_sum + cu);
+        float4 bg = make_float4(0.0f, 0.0f, 0.0f, 0.0f), bu = bg;
+        if (BIAS) {
+          bg = *reinterpret_cast<const float4*>(lds_b + cg);
+          bu = *reinterpret_cast<const float4*>(lds_b + cu);
+        }
+        const float swg_[4] = {swg.x, swg.y, swg.z, swg.w}, smg_[4] = {smg.x, smg.y, smg.z, smg.w};
+        const float swu_[4] = {swu.x, swu.y, swu.z, swu.w}, smu_[4] = {smu.x, smu.y, smu.z, smu.w};
+        const float bg_[4] = {bg.x, bg.y, bg.z, bg.w}, bu_[4] = {bu.x, bu.y, bu.z, bu.w};
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          float gv[4], uv[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            // Operation order of kernel/w4a4.cu:74-77, as in the plain epilogue.
+            gv[v] = fmaf(zr[i], smg_[v], (float)acc[i][j][4 * q + v]) * sxr[i];
+            gv[v] = gv[v] * swg_[v];
+            uv[v] = fmaf(zr[i], smu_[v], (float)acc[i][j + 2][4 * q + v]) * sxr[i];
+            uv[v] = uv[v] * swu_[v];
+            if (BIAS) {
+              gv[v] = gv[v] + bg_[v];
+              uv[v] = uv[v] + bu_[v];
+            }
+          }
+          uint2 pk;
+          pk.x = silu_mul_f16x2(pack_h2(gv[0], gv[1]), pack_h2(uv[0], uv[1]));
+          pk.y = silu_mul_f16x2(pack_h2(gv[2], gv[3]), pack_h2(uv[2], uv[3]));
+          const int r = i * 32 + rl;
+          *reinterpret_cast<uint2*>(tile + r * HRB + 16 * ((4 * j + q) ^ (r & 7)) + 8 * half) = pk;
+        }
+      }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __half* const hout = static_cast<__half*>(g.out);
+    const int64_t NH = g.N / 2;
+    const int c = el % HCPR;
+    const int64_t hcol = n0 / 2 + wn * 64 + 8 * c;
+    const bool whole = m0 + kTileM <= g.M && n0 + BN <= g.N;
+    uint8_t* const obase =
+        reinterpret_cast<uint8_t*>(hout) + 2 * ((m0 + wm * 128) * NH + n0 / 2 + wn * 64);
+    const uint32_t out_off = (uint32_t)(2 * ((el / HCPR) * NH + 8 * c));
+    constexpr int kBatch = 8;
+#pragma unroll
+    for (int sb = 0; sb < 128 / HRPI; sb += kBatch) {
+      uint4 v[kBatch];
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        const int sr = sb + t;
+        const int r = HRPI * sr + el / HCPR;
+        v[t] = *reinterpret_cast<const uint4*>(tile + r * HRB + 16 * (c ^ (r & 7)));
+        if (sr & 1) {  // bit 3 of r: halves stored swapped
+          const uint32_t x = v[t].x, y = v[t].y;
+          v[t].x = v[t].z;
+          v[t].y = v[t].w;
+          v[t].z = x;
+          v[t].w = y;
+        }
+      }
+      if (whole) {
+#pragma unroll
+        for (int t = 0; t < kBatch; ++t)
+          store_stream(v[t], obase + 2 * (int64_t)(HRPI * (sb + t)) * NH + out_off);
+      } else {
+#pragma unroll
+        for (int t = 0; t < kBatch; ++t) {
+          const int64_t row = m0 + wm * 128 + HRPI * (sb + t) + el / HCPR;
+          if (row < g.M && hcol < NH) store_stream(v[t], hout + row * NH + hcol);
+        }
+      }
+    }
+    return;
+  }
   // The wave's 128 x TN fp16 tile in LDS: row r (RB = 2 TN bytes, CPR 16-byte
   // chunks) holds chunk c at position c ^ (r % CPR), the two 8-byte halves of a
   // chunk swapped in rows with bit log2(CPR) set, so that a half-wave's 8-byte
@@ -442,6 +537,20 @@ int launch_wide_gemm(GemmArgs g, int bn, hipStream_t stream) {
     DSCQ_WIDE(128)
   }
 #undef DSCQ_WIDE
+  return launch_status("w4a4_gemm_wide_kernel");
+}
+
+int launch_wide_gemm_gated(GemmArgs g, hipStream_t stream) {
+  if (!wide_gemm_fits(g) || g.N % 128 != 0)
+    return fail("internal: shape outside the gated wide-tile GEMM");
+  g.tiles_n = (int)((g.N + 255) / 256);
+  const int64_t nblocks = ((g.M + kTileM - 1) / kTileM) * g.tiles_n;
+  if (nblocks > 0x7FFFFFFF) return fail("matmul_silu_mul: grid too large");
+  const dim3 grid((unsigned)nblocks), block(64 * kWaves);
+  if (g.bias)
+    launch((w4a4_gemm_wide_kernel<256, true, true>), grid, block, stream, g);
+  else
+    launch((w4a4_gemm_wide_kernel<256, false, true>), grid, block, stream, g);
   return launch_status("w4a4_gemm_wide_kernel");
 }
 

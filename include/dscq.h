@@ -271,8 +271,9 @@ int dscq_time_next_kernel(void* start, void* stop);
 
 /*
  * GEMM kernel choice for this thread's later dscq_matmul / dscq_matmul_ws /
- * dscq_matmul_noalloc calls (no reference counterpart; the analogue of the
- * reference's force_decode for the dense kernels, for tests and measurement):
+ * dscq_matmul_noalloc / dscq_matmul_silu_mul calls (no reference counterpart;
+ * the analogue of the reference's force_decode for the dense kernels, for
+ * tests and measurement):
  *   0  automatic (the default): for fp16 output without raw accumulators the
  *      wide-tile kernel (256 x 256 tiles, one wave per SIMD) when its tiles
  *      fill at least three quarters of a round of one tile per compute unit
@@ -284,6 +285,9 @@ int dscq_time_next_kernel(void* start, void* stop);
  *   2  never the wide-tile kernel;
  *   3, 4  the wide-tile kernel wherever it applies, with 256 x 256 / 256 x 128
  *      tiles.
+ * dscq_matmul_silu_mul (M > 16) follows the same choices with 256 x 256 tiles
+ * only: settings 1 and 3 and the automatic rule may take the wide-tile kernel,
+ * 4 takes the pipelined kernel.
  * Every kernel gives the same results.  Returns the previous setting, or
  * DSCQ_EINVAL for another value.
  */

@@ -105,6 +105,22 @@ def test_workloads_are_well_formed():
         assert M > 0 and N % 8 == 0 and K % 128 == 0 and rot in (0, 128), name
 
 
+def test_kernel_names_follow_the_dispatch_rule():
+    """bench.py's restatement of the library's dense and gated GEMM choice at
+    the configured shapes and a few around the rule's edges."""
+    assert bench.gemm_kernel_name(2048, 4096, 4096, "auto") == "w4a4_gemm_pipe_kernel"
+    assert bench.gemm_kernel_name(4096, 8192, 8192, "auto") == "w4a4_gemm_wide_kernel<256>"
+    assert bench.gemm_kernel_name(4096, 8192, 8192, "pipe") == "w4a4_gemm_pipe_kernel"
+    assert bench.gemm_kernel_name(2048, 4096, 4096, "wide128") == "w4a4_gemm_wide_kernel<128>"
+    # the gated GEMM (N = h columns): 172 wide tiles (2/3 of a round) stay pipelined,
+    # 224 (7/8) and 688 (2.7 rounds) go wide, 344 (1.3 rounds) stay pipelined
+    assert bench.gated_kernel_name(512, 11008, 4096, "auto") == "w4a4_gemm_pipe_kernel"
+    assert bench.gated_kernel_name(512, 14336, 4096, "auto") == "w4a4_gemm_wide_kernel<256>"
+    assert bench.gated_kernel_name(2048, 11008, 4096, "auto") == "w4a4_gemm_wide_kernel<256>"
+    assert bench.gated_kernel_name(1024, 11008, 4096, "auto") == "w4a4_gemm_pipe_kernel"
+    assert bench.gated_kernel_name(512, 11008, 4096, "wide128") == "w4a4_gemm_pipe_kernel"
+
+
 def test_more_than_one_gpu_is_refused():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)

@@ -98,6 +98,40 @@ def test_matmul_silu_mul_matches_unfused_path(gpu, M, K, N, bias):
     assert torch.equal(p, p_ref) and torch.equal(s_, s_ref) and torch.equal(z, z_ref)
 
 
+@pytest.mark.parametrize("M,K,N,bias", [(512, 4096, 11008, True), (512, 4096, 11008, False),
+                                        (1000, 2048, 2880, True), (64, 4096, 1024, False),
+                                        (256, 512, 64, True), (300, 8192, 4160, False)])
+def test_matmul_silu_mul_wide_tiles(gpu, M, K, N, bias):
+    """The gated GEMM on the wide-tile kernel (dscq_set_gemm_kernel(3): 256 x 256
+    tiles, each wave's 128 columns the gate and up rows of 64 outputs; partial
+    tiles in M and N, one to 32 slices) gives the unfused path's h bit for bit,
+    and the pipelined kernel's."""
+    from tests.test_gpu_wide import gemm_kernel
+    print(f"matmul_silu_mul wide case M{M} K{K} N{N} bias{bias}", flush=True)
+    x = torch.from_numpy(activations(M, K, seed=M + 3 * K)).to(gpu)
+    wg = torch.from_numpy(weights(N, K, seed=21)).to(gpu)
+    wu = torch.from_numpy(weights(N, K, seed=22)).to(gpu)
+    pg, swg, sg = w4a4.pack_weight(wg, 1.0, 0)
+    pu, swu, su = w4a4.pack_weight(wu, 1.0, 0)
+    gen = torch.Generator().manual_seed(N + 1)
+    bg = (torch.randn(N, generator=gen) * 0.1).half().to(gpu) if bias else None
+    bu = (torch.randn(N, generator=gen) * 0.1).half().to(gpu) if bias else None
+    empty = torch.empty(0, dtype=torch.float16, device=gpu)
+    pa, sx, zx = w4a4.quantize(x, 1.0, True, 0)
+    gu, _ = w4a4.matmul(pa, torch.cat([pg, pu]), sx, zx, torch.cat([swg, swu]),
+                        torch.cat([sg, su]), torch.cat([bg, bu]) if bias else empty, M, 2 * N)
+    _, _, _, h_ref = w4a4.silu_mul_quantize(gu, 1.0, 0, return_h=True)
+    il = w4a4.interleave_gate_up
+    args = (pa, il(pg, pu), sx, zx, il(swg, swu), il(sg, su), il(bg, bu) if bias else empty, M, N)
+    with gemm_kernel(3):
+        h_wide = w4a4.matmul_silu_mul(*args)
+    with gemm_kernel(2):
+        h_pipe = w4a4.matmul_silu_mul(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(h_wide, h_ref)
+    assert torch.equal(h_pipe, h_ref)
+
+
 def test_matmul_silu_mul_rejects_bad_shapes(gpu):
     pa = torch.zeros((64, 64), dtype=torch.uint8, device=gpu)
     sx = torch.ones(64, device=gpu)

@@ -6,8 +6,8 @@ change between replays.  Covered: rotate+quantize+pack -> pipelined GEMM
 (prefill shape class, the prefill shape itself) and -> wide-tile GEMM (forced
 at both tile widths, and by the automatic rule), quantize -> skinny-M GEMM (16
 tokens, one and three column tiles per workgroup), the fused decode kernel (one
-and three tiles per workgroup, both product forms), and the SiLU-gated
-requantization.
+and three tiles per workgroup, both product forms), the SiLU-gated
+requantization, and the gated GEMM on the wide-tile and pipelined kernels.
 """
 import numpy as np
 import pytest
@@ -114,4 +114,27 @@ def test_silu_mul_quantize_graph(gpu):
     rng = np.random.default_rng(7)
     xs = [torch.from_numpy((rng.standard_normal((M, 2 * N)) * 2).astype(np.float16)).to(gpu)
           for _ in range(3)]
+    _replay_and_compare(run, xs)
+
+
+@pytest.mark.parametrize("M,K,N,which", [(512, 4096, 2048, 3), (512, 4096, 2048, 2)])
+def test_quantize_matmul_silu_mul_graph(gpu, M, K, N, which):
+    """The gated GEMM (gate|up with the SiLU-gated epilogue) captured and
+    replayed on the wide-tile kernel (forced) and on the pipelined kernel."""
+    from tests.test_gpu_wide import gemm_kernel
+    print(f"graph quantize+matmul_silu_mul M{M} K{K} N{N} kernel{which}", flush=True)
+    pg, swg, sg = w4a4.pack_weight(torch.from_numpy(weights(N, K, seed=31)).to(gpu), 1.0, 0)
+    pu, swu, su = w4a4.pack_weight(torch.from_numpy(weights(N, K, seed=32)).to(gpu), 1.0, 0)
+    il = w4a4.interleave_gate_up
+    b, sw, sums = il(pg, pu), il(swg, swu), il(sg, su)
+    empty = torch.empty(0, dtype=torch.float16, device=gpu)
+
+    def run(x):
+        with gemm_kernel(which):
+            pa, sx, zx = w4a4.quantize(x, 1.0, True, 0)
+            h = w4a4.matmul_silu_mul(pa, b, sx, zx, sw, sums, empty, M, N)
+        return [h, pa]
+
+    xs = [torch.from_numpy(activations(M, K, seed=s).astype(np.float16)).to(gpu)
+          for s in (10, 11, 12)]
     _replay_and_compare(run, xs)
